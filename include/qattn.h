@@ -1,0 +1,182 @@
+/*
+ * qattn.h -- C ABI of the MI355X (gfx950) causal GQA prefill attention library.
+ *
+ * Drop-in for the attention path of the reference engine (paths are relative to the reference
+ * checkout, shihanqu/qwen3-embedding-webgpu-prepacked):
+ *
+ *   reference                                           | this ABI
+ *   ----------------------------------------------------+-------------------------------------
+ *   requestWebGPUDevice()              device.ts:6-24   | qattn_create / qattn_destroy
+ *   createBufferWithData / createBuffer device.ts:26-37 | qattn_buffer_alloc / _write / _read
+ *   CausalAttentionKernel.createRun    ops.ts:327-343   | qattn_run_create
+ *   CausalAttentionKernel.encode       ops.ts:344       | qattn_run_encode
+ *   plan.destroy() of run.ownedBuffers model.ts:108-111 | qattn_run_destroy
+ *   tiled flash attention shader       ops.ts:168-241   | kernel behind qattn_run_encode
+ *   mask predicate + tile skip         ops.ts:205-220   | qattn_debug_mask (same device code)
+ *   QKNormRopeKernel                   ops.ts:104-166   | qattn_qk_norm_rope
+ *   RoPE table                         model.ts:76-83   | built inside qattn_qk_norm_rope
+ *   last-token row of poolShader       ops.ts:357       | qattn_run_desc.o_last
+ *
+ * Fixed model geometry (model.ts:18-23, ops.ts:196): 16 query heads, 8 KV heads (query head h
+ * reads KV head h/2), head_dim 128, scale 1/sqrt(128), fp16 storage, fp32 accumulation.
+ *
+ * Conventions: every function returns QATTN_OK (0) or a negative status; the message of the
+ * last failure is available from qattn_last_error(ctx) (thread-local when ctx is NULL).
+ * Arguments are validated on the host before any launch.  A context owns one HIP stream
+ * created with the default priority; `stream == NULL` in an entry point means that stream.
+ * Device pointers are plain `void*` device addresses (from qattn_buffer_alloc or any other HIP
+ * allocation on the same device).
+ */
+#ifndef QATTN_H
+#define QATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QATTN_ABI_VERSION 1
+
+#define QATTN_Q_HEADS 16
+#define QATTN_KV_HEADS 8
+#define QATTN_HEAD_DIM 128
+#define QATTN_MAX_SEQS 65536
+
+enum qattn_status {
+  QATTN_OK = 0,
+  QATTN_EINVAL = -1, /* bad argument (shape, stride, alignment, cu_seqlens, mask) */
+  QATTN_EHIP = -2,   /* HIP runtime error */
+  QATTN_ENOMEM = -3, /* device or host allocation failed */
+  QATTN_ENODEV = -4  /* no usable gfx950 device */
+};
+
+enum qattn_mask_kind {
+  QATTN_MASK_CAUSAL = 0,       /* k <= q */
+  QATTN_MASK_PREFIX_LOCAL = 1  /* k <= q && (k < prefix || q - k < window): ops.ts:206,220 */
+};
+
+typedef struct qattn_ctx qattn_ctx;
+typedef struct qattn_run qattn_run;
+typedef void* qattn_stream_t; /* a hipStream_t */
+
+/* ---- device context  (replaces requestWebGPUDevice, device.ts:6-24) --------------------- */
+int qattn_create(int device, qattn_ctx** out);
+void qattn_destroy(qattn_ctx* ctx);
+const char* qattn_last_error(const qattn_ctx* ctx);
+int qattn_abi_version(void);
+qattn_stream_t qattn_stream(qattn_ctx* ctx);
+int qattn_synchronize(qattn_ctx* ctx);
+/* gcnArchName (e.g. "gfx950:sramecc+:xnack-") and the CU count of the context's device. */
+int qattn_device_name(qattn_ctx* ctx, char* buf, size_t len, int* cu_count);
+
+/* ---- device buffers  (replaces createBuffer / createBufferWithData, device.ts:26-37, and
+ *      queue.writeBuffer / mapAsync readback, model.ts:115-116,135) ----------------------- */
+int qattn_buffer_alloc(qattn_ctx* ctx, size_t bytes, void** dptr);
+int qattn_buffer_free(qattn_ctx* ctx, void* dptr);
+/* Synchronous on the context stream. */
+int qattn_buffer_write(qattn_ctx* ctx, void* dst, size_t offset, const void* src, size_t bytes);
+int qattn_buffer_read(qattn_ctx* ctx, const void* src, size_t offset, void* dst, size_t bytes);
+int qattn_buffer_fill_u16(qattn_ctx* ctx, void* dst, uint16_t value, size_t count);
+
+/* ---- attention operator  (replaces CausalAttentionKernel, ops.ts:318-345) ---------------- */
+typedef struct qattn_run_desc {
+  /* fp16 device tensors.  Token t of the packed batch is row t.  Head h of Q/O is the 128
+   * halves at element t*row_stride + h*128; KV head g of K at t*k_row_stride + g*128 and of V at
+   * v_offset + t*v_row_stride + g*128 (the reference reads V in place from qkvRaw with
+   * value_stride 4096 / value_offset 3072, model.ts:95).  Pointers 16-byte aligned; strides and
+   * v_offset multiples of 8 elements; q/o strides >= 2048, k/v strides >= 1024. */
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  int64_t q_row_stride, k_row_stride, v_row_stride, o_row_stride, v_offset;
+  /* Host array of nseq+1 non-decreasing token offsets starting at 0: sequence i is rows
+   * cu_seqlens[i] .. cu_seqlens[i+1]-1 and attends only within itself (positions restart at 0).
+   * Replaces the reference's padded [batch, sequence] layout (ops.ts:200,213).  Copied. */
+  const int32_t* cu_seqlens;
+  int32_t nseq;
+  int32_t mask;    /* enum qattn_mask_kind */
+  int32_t prefix;  /* PREFIX_LOCAL: keys 0..prefix-1 always visible (reference 176) */
+  int32_t window;  /* PREFIX_LOCAL: keys q-window+1..q visible (reference 432) */
+  /* Optional fp16 [nseq][16*128] device output: row i receives O of token cu_seqlens[i+1]-1,
+   * the row the reference's last-token pool reads (ops.ts:357).  NULL to skip. */
+  void* o_last;
+} qattn_run_desc;
+
+/* Plans the launch (validates, builds the work list of (sequence, kv_head, query block) items
+ * heaviest first, uploads it) and returns a run that owns its device work list. */
+int qattn_run_create(qattn_ctx* ctx, const qattn_run_desc* desc, qattn_run** out);
+/* Enqueues the attention kernel of a run on `stream` (NULL: the context stream). */
+int qattn_run_encode(qattn_run* run, qattn_stream_t stream);
+/* Re-points a run at other tensors of the same shape (layers sharing one packing). */
+int qattn_run_rebind(qattn_run* run, const void* q, const void* k, const void* v, void* o,
+                     void* o_last);
+void qattn_run_destroy(qattn_run* run);
+
+typedef struct qattn_run_info {
+  int64_t tokens;           /* sum of sequence lengths */
+  int64_t pairs;            /* retained (query, key) pairs summed over sequences */
+  int64_t flops;            /* 4 * 128 * 16 * pairs: QK^T and PV over all query heads */
+  int64_t bytes;            /* 12288 * tokens (+ 4096 per sequence with o_last): Q,K,V,O fp16 */
+  int32_t work_items;       /* workgroups launched */
+  int32_t block_queries;    /* query positions per work item */
+  int64_t tile_pairs;       /* (query, key) pairs inside the MFMA tiles computed, per query head */
+} qattn_run_info;
+int qattn_run_get_info(const qattn_run* run, qattn_run_info* info);
+
+/* Host-only planning (no device needed): validates `desc` exactly as qattn_run_create does and
+ * reports the work list a run would launch, in launch order.  Each item is four int32:
+ * {first token of the sequence, sequence length, query block, sequence<<4 | kv_head}.
+ * `items` may be NULL (count only); `*count` receives the number of items, `info` (optional) the
+ * run's figures.  Fails with QATTN_EINVAL if `capacity` is too small for a non-NULL `items`. */
+int qattn_plan_describe(const qattn_run_desc* desc, int32_t* items, int32_t capacity,
+                        int32_t* count, qattn_run_info* info);
+
+/* One-shot: create, encode, wait for completion, destroy. */
+int qattn_prefill(qattn_ctx* ctx, const qattn_run_desc* desc, qattn_stream_t stream);
+
+/* ---- mask check  (same device predicate and key-tile iterator as the attention kernel) ---- */
+/* Writes the retained-key bitmask of one sequence of length L to host memory: word
+ * q*ceil(L/32) + k/32, bit k%32 set iff the attention kernel visits key k for query q and keeps
+ * it.  Must equal the reference predicate ops.ts:205-209,219-220 bit for bit. */
+int qattn_debug_mask(qattn_ctx* ctx, int32_t L, int32_t mask, int32_t prefix, int32_t window,
+                     uint32_t* host_bits);
+
+/* Host evaluation of the same iteration code (attn_common.h is compiled for host and device):
+ * no device needed.  Same output layout as qattn_debug_mask. */
+int qattn_plan_mask(int32_t L, int32_t mask, int32_t prefix, int32_t window, uint32_t* host_bits);
+
+/* ---- producer: QK RMSNorm + RoPE  (replaces QKNormRopeKernel, ops.ts:104-166) ------------- */
+/* In place on fp16 rows: for each token and each of `heads` 128-wide vectors at element
+ * t*row_stride + col0 + h*128: RMSNorm (eps, gain `weight` f32[128] device or NULL for 1), then
+ * NeoX rotate-half RoPE with theta at the token's position inside its sequence. */
+int qattn_qk_norm_rope(qattn_ctx* ctx, void* x, int64_t row_stride, int64_t col0, int32_t heads,
+                       const int32_t* cu_seqlens, int32_t nseq, const float* weight, double eps,
+                       double theta, qattn_stream_t stream);
+
+/* ---- synthetic inputs ---------------------------------------------------------------------- */
+/* Element (r, c), r < rows, c < row_elems, at dst[r*row_stride + c] receives
+ * f16((float)N(0,1)) where the normal has index e = r*row_elems + c: Box-Muller over the pair
+ * e>>1 of the SplitMix64(seed) stream (outputs e&~1 and e|1), cos for even e, sin for odd e. */
+int qattn_fill_normal(qattn_ctx* ctx, void* dst, int64_t rows, int64_t row_elems,
+                      int64_t row_stride, uint64_t seed, qattn_stream_t stream);
+/* Seeded Q/K/V of one (config, layer): raw N(0,1) fp16 Q [T,16,128], K [T,8,128],
+ * V [T,8,128] (seeds 0x51574E33_00000000 | config<<16 | layer<<8 | tensor), then
+ * qattn_qk_norm_rope on Q and K (unit gain, eps 1e-6, theta 1e6). */
+int qattn_gen_qkv(qattn_ctx* ctx, uint32_t config, uint32_t layer, const int32_t* cu_seqlens,
+                  int32_t nseq, void* q, int64_t q_row_stride, void* k, int64_t k_row_stride,
+                  void* v, int64_t v_row_stride, qattn_stream_t stream);
+
+/* ---- timing (hosts without a HIP runtime: Node, ctypes) ------------------------------------ */
+typedef void* qattn_event_t;
+int qattn_event_create(qattn_ctx* ctx, qattn_event_t* ev);
+int qattn_event_record(qattn_event_t ev, qattn_stream_t stream);
+int qattn_event_elapsed_ms(qattn_event_t start, qattn_event_t stop, float* ms);
+int qattn_event_destroy(qattn_event_t ev);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

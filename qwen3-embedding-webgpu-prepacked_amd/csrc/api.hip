@@ -1,0 +1,611 @@
+// api.hip -- the C ABI declared in include/qattn.h: context, buffers, the attention operator
+// (planner + launch), the mask check, the QK-norm/RoPE producer and the input generator.
+//
+// Planner (replaces CausalAttentionKernel.createRun, src/webgpu/ops.ts:327-343): the reference
+// bakes [batch, sequence, heads, value_stride, value_offset] into a uniform buffer and
+// dispatches ceil(S/16) x batch*16 workgroups over a padded batch.  Here a run holds a device
+// work list of (sequence, KV head, 64-query block) items built from cu_seqlens: no padded rows,
+// both heads of a GQA group per item, heaviest items first so the longest causal rows start
+// early, and one launch per layer regardless of sequence length (the reference switches to a
+// chunked two-pass path above 8192 tokens, ops.ts:328-342; this kernel has no such limit).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/qattn.h"
+#include "attn_common.h"
+
+namespace qattn {
+typedef _Float16 half_t;
+struct AttnParams {
+  const half_t* q;
+  const half_t* k;
+  const half_t* v;
+  half_t* o;
+  half_t* o_last;
+  int64_t q_stride, k_stride, v_stride, o_stride;
+  const WorkItem* work;
+  int32_t n_work;
+  MaskSpec mask;
+  float scale_log2;
+};
+hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream);
+hipError_t launch_debug_mask(int S, MaskSpec mask, uint32_t* bits, int words_per_row,
+                             hipStream_t stream);
+hipError_t launch_fill_normal(half_t* dst, int64_t rows, int64_t row_elems, int64_t row_stride,
+                              uint64_t seed, hipStream_t stream);
+hipError_t launch_qk_norm_rope(half_t* x, int64_t row_stride, int64_t col0, int heads,
+                               const int32_t* cu_dev, int nseq, int64_t T, const float* weight,
+                               double eps, const float* rope_cos, const float* rope_sin,
+                               hipStream_t stream);
+}  // namespace qattn
+
+using namespace qattn;
+
+struct qattn_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string last_error;
+  std::mutex mu;
+};
+
+struct qattn_run {
+  qattn_ctx* ctx = nullptr;
+  AttnParams params{};
+  WorkItem* work_dev = nullptr;
+  int64_t v_offset = 0;
+  bool has_o_last = false;
+  qattn_run_info info{};
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(qattn_ctx* ctx, int code, const char* fmt, ...) __attribute__((format(printf, 3, 4)));
+int fail(qattn_ctx* ctx, int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  if (ctx) {
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    ctx->last_error = buf;
+  }
+  return code;
+}
+
+#define HIP_TRY(ctx, expr)                                                                   \
+  do {                                                                                       \
+    hipError_t e_ = (expr);                                                                  \
+    if (e_ != hipSuccess)                                                                    \
+      return fail((ctx), QATTN_EHIP, "%s failed: %s", #expr, hipGetErrorString(e_));        \
+  } while (0)
+
+struct DeviceGuard {
+  int prev = -1;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (prev != dev) (void)hipSetDevice(dev);
+  }
+  ~DeviceGuard() {
+    if (prev >= 0) (void)hipSetDevice(prev);
+  }
+};
+
+hipStream_t pick_stream(qattn_ctx* ctx, qattn_stream_t s) {
+  return s ? reinterpret_cast<hipStream_t>(s) : ctx->stream;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int validate_cu(qattn_ctx* ctx, const int32_t* cu, int32_t nseq) {
+  if (!cu) return fail(ctx, QATTN_EINVAL, "cu_seqlens is NULL");
+  if (nseq < 1 || nseq > QATTN_MAX_SEQS)
+    return fail(ctx, QATTN_EINVAL, "nseq=%d outside [1, %d]", nseq, QATTN_MAX_SEQS);
+  if (cu[0] != 0) return fail(ctx, QATTN_EINVAL, "cu_seqlens[0]=%d, expected 0", cu[0]);
+  for (int32_t i = 0; i < nseq; ++i)
+    if (cu[i + 1] < cu[i])
+      return fail(ctx, QATTN_EINVAL, "cu_seqlens not non-decreasing at %d (%d > %d)", i, cu[i],
+                  cu[i + 1]);
+  return QATTN_OK;
+}
+
+int validate_desc(qattn_ctx* ctx, const qattn_run_desc* d) {
+  if (!d) return fail(ctx, QATTN_EINVAL, "desc is NULL");
+  if (!d->q || !d->k || !d->v || !d->o) return fail(ctx, QATTN_EINVAL, "q/k/v/o must be non-NULL");
+  if (!aligned16(d->q) || !aligned16(d->k) || !aligned16(d->v) || !aligned16(d->o) ||
+      (d->o_last && !aligned16(d->o_last)))
+    return fail(ctx, QATTN_EINVAL, "q/k/v/o/o_last must be 16-byte aligned");
+  if (d->q_row_stride < kQHeads * kHeadDim || d->o_row_stride < kQHeads * kHeadDim ||
+      d->k_row_stride < kKVHeads * kHeadDim || d->v_row_stride < kKVHeads * kHeadDim)
+    return fail(ctx, QATTN_EINVAL,
+                "row strides too small (q %lld, k %lld, v %lld, o %lld; need q,o >= 2048 and "
+                "k,v >= 1024)",
+                (long long)d->q_row_stride, (long long)d->k_row_stride,
+                (long long)d->v_row_stride, (long long)d->o_row_stride);
+  if ((d->q_row_stride | d->k_row_stride | d->v_row_stride | d->o_row_stride | d->v_offset) & 7)
+    return fail(ctx, QATTN_EINVAL, "row strides and v_offset must be multiples of 8 elements");
+  if (d->v_offset < 0) return fail(ctx, QATTN_EINVAL, "v_offset must be >= 0");
+  if (d->mask != QATTN_MASK_CAUSAL && d->mask != QATTN_MASK_PREFIX_LOCAL)
+    return fail(ctx, QATTN_EINVAL, "unknown mask kind %d", d->mask);
+  if (d->mask == QATTN_MASK_PREFIX_LOCAL) {
+    if (d->prefix < 0 || d->window < 0)
+      return fail(ctx, QATTN_EINVAL, "prefix (%d) and window (%d) must be >= 0", d->prefix, d->window);
+    if (d->prefix == 0 && d->window == 0)
+      return fail(ctx, QATTN_EINVAL, "prefix and window are both 0: no query would see a key");
+  }
+  int rc = validate_cu(ctx, d->cu_seqlens, d->nseq);
+  if (rc) return rc;
+  const int64_t T = d->cu_seqlens[d->nseq];
+  const int64_t max_rows = (int64_t)1 << 31;
+  if (T * d->q_row_stride >= max_rows * 64 || T >= max_rows)
+    return fail(ctx, QATTN_EINVAL, "too many tokens (%lld)", (long long)T);
+  return QATTN_OK;
+}
+
+int64_t pairs_of(int64_t L, const MaskSpec& m) {
+  // Closed form of the retained-pair count (sum over q of |{k : retained(q,k)}|).
+  if (L <= 0) return 0;
+  if (m.kind == 0) return L * (L + 1) / 2;
+  int64_t total = 0;
+  const int64_t ps = std::min<int64_t>(L, m.prefix), ws = std::min<int64_t>(L, m.window);
+  for (int64_t q = 0; q < L; ++q) {
+    // keys [0, min(q, ps-1)] U [max(0, q-ws+1), q]
+    const int64_t a = std::min<int64_t>(q + 1, ps);    // prefix part
+    const int64_t wlo = std::max<int64_t>(0, q - ws + 1);
+    const int64_t b = q + 1 - std::max<int64_t>(wlo, a);  // window part not already counted
+    total += a + std::max<int64_t>(0, b);
+  }
+  return total;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qattn_abi_version(void) { return QATTN_ABI_VERSION; }
+
+const char* qattn_last_error(const qattn_ctx* ctx) {
+  if (ctx) return ctx->last_error.c_str();
+  return g_last_error.c_str();
+}
+
+int qattn_create(int device, qattn_ctx** out) {
+  if (!out) return fail(nullptr, QATTN_EINVAL, "out is NULL");
+  *out = nullptr;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n <= 0) return fail(nullptr, QATTN_ENODEV, "no HIP device (%s)", hipGetErrorString(e));
+  if (device < 0 || device >= n) return fail(nullptr, QATTN_EINVAL, "device %d outside [0, %d)", device, n);
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess) return fail(nullptr, QATTN_EHIP, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(nullptr, QATTN_ENODEV, "device %d is %s; this library is built for gfx950 only",
+                device, prop.gcnArchName);
+  auto* ctx = new (std::nothrow) qattn_ctx();
+  if (!ctx) return fail(nullptr, QATTN_ENOMEM, "out of host memory");
+  ctx->device = device;
+  DeviceGuard g(device);
+  e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete ctx;
+    return fail(nullptr, QATTN_EHIP, "hipStreamCreate: %s", hipGetErrorString(e));
+  }
+  *out = ctx;
+  return QATTN_OK;
+}
+
+void qattn_destroy(qattn_ctx* ctx) {
+  if (!ctx) return;
+  {
+    DeviceGuard g(ctx->device);
+    if (ctx->stream) {
+      (void)hipStreamSynchronize(ctx->stream);
+      (void)hipStreamDestroy(ctx->stream);
+    }
+  }
+  delete ctx;
+}
+
+qattn_stream_t qattn_stream(qattn_ctx* ctx) { return ctx ? ctx->stream : nullptr; }
+
+int qattn_synchronize(qattn_ctx* ctx) {
+  if (!ctx) return fail(nullptr, QATTN_EINVAL, "ctx is NULL");
+  DeviceGuard g(ctx->device);
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  return QATTN_OK;
+}
+
+int qattn_device_name(qattn_ctx* ctx, char* buf, size_t len, int* cu_count) {
+  if (!ctx) return fail(nullptr, QATTN_EINVAL, "ctx is NULL");
+  hipDeviceProp_t prop;
+  HIP_TRY(ctx, hipGetDeviceProperties(&prop, ctx->device));
+  if (buf && len) {
+    std::strncpy(buf, prop.gcnArchName, len - 1);
+    buf[len - 1] = 0;
+  }
+  if (cu_count) *cu_count = prop.multiProcessorCount;
+  return QATTN_OK;
+}
+
+// ---- buffers ----------------------------------------------------------------------------------
+
+int qattn_buffer_alloc(qattn_ctx* ctx, size_t bytes, void** dptr) {
+  if (!ctx || !dptr) return fail(ctx, QATTN_EINVAL, "ctx/dptr is NULL");
+  *dptr = nullptr;
+  DeviceGuard g(ctx->device);
+  hipError_t e = hipMalloc(dptr, bytes ? bytes : 16);
+  if (e != hipSuccess) return fail(ctx, QATTN_ENOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+  return QATTN_OK;
+}
+
+int qattn_buffer_free(qattn_ctx* ctx, void* dptr) {
+  if (!ctx) return fail(nullptr, QATTN_EINVAL, "ctx is NULL");
+  if (!dptr) return QATTN_OK;
+  DeviceGuard g(ctx->device);
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  HIP_TRY(ctx, hipFree(dptr));
+  return QATTN_OK;
+}
+
+int qattn_buffer_write(qattn_ctx* ctx, void* dst, size_t offset, const void* src, size_t bytes) {
+  if (!ctx || !dst || (!src && bytes)) return fail(ctx, QATTN_EINVAL, "NULL argument");
+  if (!bytes) return QATTN_OK;
+  DeviceGuard g(ctx->device);
+  HIP_TRY(ctx, hipMemcpyAsync(static_cast<char*>(dst) + offset, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  return QATTN_OK;
+}
+
+int qattn_buffer_read(qattn_ctx* ctx, const void* src, size_t offset, void* dst, size_t bytes) {
+  if (!ctx || !src || (!dst && bytes)) return fail(ctx, QATTN_EINVAL, "NULL argument");
+  if (!bytes) return QATTN_OK;
+  DeviceGuard g(ctx->device);
+  HIP_TRY(ctx, hipMemcpyAsync(dst, static_cast<const char*>(src) + offset, bytes, hipMemcpyDeviceToHost, ctx->stream));
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  return QATTN_OK;
+}
+
+int qattn_buffer_fill_u16(qattn_ctx* ctx, void* dst, uint16_t value, size_t count) {
+  if (!ctx || (!dst && count)) return fail(ctx, QATTN_EINVAL, "NULL argument");
+  if (!count) return QATTN_OK;
+  DeviceGuard g(ctx->device);
+  HIP_TRY(ctx, hipMemsetD16Async(reinterpret_cast<hipDeviceptr_t>(dst), value, count, ctx->stream));
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  return QATTN_OK;
+}
+
+// ---- attention operator -----------------------------------------------------------------------
+
+}  // extern "C"
+
+namespace {
+
+// The planner: validated description -> work items in launch order + run figures.
+int plan_work(qattn_ctx* ctx, const qattn_run_desc* d, std::vector<WorkItem>* out,
+              qattn_run_info* info_out, MaskSpec* mask_out) {
+  int rc = validate_desc(ctx, d);
+  if (rc) return rc;
+  const MaskSpec mask{d->mask, d->mask == QATTN_MASK_PREFIX_LOCAL ? d->prefix : 0,
+                      d->mask == QATTN_MASK_PREFIX_LOCAL ? d->window : 0};
+  struct Item {
+    WorkItem w;
+    int cost;
+  };
+  std::vector<Item> items;
+  qattn_run_info info{};
+  info.block_queries = kBlockQ;
+  for (int32_t s = 0; s < d->nseq; ++s) {
+    const int start = d->cu_seqlens[s];
+    const int L = d->cu_seqlens[s + 1] - start;
+    info.tokens += L;
+    info.pairs += pairs_of(L, mask);
+    for (int qb = 0; qb * kBlockQ < L; ++qb) {
+      const int q0 = qb * kBlockQ, q1 = std::min(L, q0 + kBlockQ) - 1;
+      const TileRanges tr = key_tiles(q0, q1, L, mask);
+      // MFMA tile work of one query head: the wavefronts holding rows [q0, q0+31] and
+      // [q0+32, q0+63] each compute the tiles tile_any() admits for their rows.
+      int cost = 0;
+      for (int half = 0; half < 2; ++half) {
+        const int wq0 = q0 + half * kWaveQ;
+        if (wq0 >= L) continue;
+        const int wq1 = std::min(L - 1, wq0 + kWaveQ - 1);
+        for (int i = 0; i < tr.count(); ++i)
+          if (tile_any(tr.at(i) * kTileK, wq0, wq1, L, mask)) ++cost;
+      }
+      info.tile_pairs += (int64_t)cost * kWaveQ * kTileK;
+      for (int g = 0; g < kKVHeads; ++g)
+        items.push_back({WorkItem{start, L, qb, (s << 4) | g}, tr.count() * 256 + cost});
+    }
+  }
+  // Heaviest first: most key tiles walked, then most wavefront tiles computed; stable so
+  // equal items keep sequence/head order.
+  std::stable_sort(items.begin(), items.end(), [](const Item& a, const Item& b) { return a.cost > b.cost; });
+  info.work_items = (int32_t)items.size();
+  info.flops = 4ll * kHeadDim * kQHeads * info.pairs;
+  info.bytes = 12288ll * info.tokens + (d->o_last ? 4096ll * d->nseq : 0);
+  out->resize(items.size());
+  for (size_t i = 0; i < items.size(); ++i) (*out)[i] = items[i].w;
+  if (info_out) *info_out = info;
+  if (mask_out) *mask_out = mask;
+  return QATTN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qattn_plan_describe(const qattn_run_desc* desc, int32_t* items, int32_t capacity,
+                        int32_t* count, qattn_run_info* info) {
+  if (!count) return fail(nullptr, QATTN_EINVAL, "count is NULL");
+  std::vector<WorkItem> work;
+  qattn_run_info inf{};
+  int rc = plan_work(nullptr, desc, &work, &inf, nullptr);
+  if (rc) return rc;
+  *count = (int32_t)work.size();
+  if (info) *info = inf;
+  if (items) {
+    if (capacity < (int32_t)work.size())
+      return fail(nullptr, QATTN_EINVAL, "capacity %d < %zu work items", capacity, work.size());
+    std::memcpy(items, work.data(), work.size() * sizeof(WorkItem));
+  }
+  return QATTN_OK;
+}
+
+int qattn_run_create(qattn_ctx* ctx, const qattn_run_desc* d, qattn_run** out) {
+  if (!ctx || !out) return fail(ctx, QATTN_EINVAL, "ctx/out is NULL");
+  *out = nullptr;
+  std::vector<WorkItem> host;
+  qattn_run_info info{};
+  MaskSpec mask{};
+  int rc = plan_work(ctx, d, &host, &info, &mask);
+  if (rc) return rc;
+
+  auto* run = new (std::nothrow) qattn_run();
+  if (!run) return fail(ctx, QATTN_ENOMEM, "out of host memory");
+  run->ctx = ctx;
+  run->info = info;
+  run->v_offset = d->v_offset;
+  run->has_o_last = d->o_last != nullptr;
+  if (!host.empty()) {
+    DeviceGuard g(ctx->device);
+    hipError_t e = hipMalloc(&run->work_dev, host.size() * sizeof(WorkItem));
+    if (e != hipSuccess) {
+      delete run;
+      return fail(ctx, QATTN_ENOMEM, "hipMalloc(work list): %s", hipGetErrorString(e));
+    }
+    e = hipMemcpy(run->work_dev, host.data(), host.size() * sizeof(WorkItem), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      (void)hipFree(run->work_dev);
+      delete run;
+      return fail(ctx, QATTN_EHIP, "hipMemcpy(work list): %s", hipGetErrorString(e));
+    }
+  }
+  AttnParams& p = run->params;
+  p.q = static_cast<const half_t*>(d->q);
+  p.k = static_cast<const half_t*>(d->k);
+  p.v = static_cast<const half_t*>(d->v) + d->v_offset;
+  p.o = static_cast<half_t*>(d->o);
+  p.o_last = static_cast<half_t*>(d->o_last);
+  p.q_stride = d->q_row_stride;
+  p.k_stride = d->k_row_stride;
+  p.v_stride = d->v_row_stride;
+  p.o_stride = d->o_row_stride;
+  p.work = run->work_dev;
+  p.n_work = (int32_t)host.size();
+  p.mask = mask;
+  p.scale_log2 = (float)(1.4426950408889634 / std::sqrt(128.0));
+  *out = run;
+  return QATTN_OK;
+}
+
+int qattn_run_encode(qattn_run* run, qattn_stream_t stream) {
+  if (!run) return fail(nullptr, QATTN_EINVAL, "run is NULL");
+  qattn_ctx* ctx = run->ctx;
+  DeviceGuard g(ctx->device);
+  HIP_TRY(ctx, launch_attn_fwd(run->params, pick_stream(ctx, stream)));
+  return QATTN_OK;
+}
+
+int qattn_run_rebind(qattn_run* run, const void* q, const void* k, const void* v, void* o,
+                     void* o_last) {
+  if (!run) return fail(nullptr, QATTN_EINVAL, "run is NULL");
+  if (!q || !k || !v || !o) return fail(run->ctx, QATTN_EINVAL, "q/k/v/o must be non-NULL");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || (o_last && !aligned16(o_last)))
+    return fail(run->ctx, QATTN_EINVAL, "q/k/v/o/o_last must be 16-byte aligned");
+  if ((o_last != nullptr) != run->has_o_last)
+    return fail(run->ctx, QATTN_EINVAL, "o_last presence must match the run's description");
+  AttnParams& p = run->params;
+  p.q = static_cast<const half_t*>(q);
+  p.k = static_cast<const half_t*>(k);
+  p.v = static_cast<const half_t*>(v) + run->v_offset;
+  p.o = static_cast<half_t*>(o);
+  p.o_last = static_cast<half_t*>(o_last);
+  return QATTN_OK;
+}
+
+void qattn_run_destroy(qattn_run* run) {
+  if (!run) return;
+  if (run->work_dev) {
+    DeviceGuard g(run->ctx->device);
+    (void)hipStreamSynchronize(run->ctx->stream);
+    (void)hipFree(run->work_dev);
+  }
+  delete run;
+}
+
+int qattn_run_get_info(const qattn_run* run, qattn_run_info* info) {
+  if (!run || !info) return fail(nullptr, QATTN_EINVAL, "NULL argument");
+  *info = run->info;
+  return QATTN_OK;
+}
+
+int qattn_prefill(qattn_ctx* ctx, const qattn_run_desc* desc, qattn_stream_t stream) {
+  qattn_run* run = nullptr;
+  int rc = qattn_run_create(ctx, desc, &run);
+  if (rc) return rc;
+  rc = qattn_run_encode(run, stream);
+  if (rc == QATTN_OK) {
+    DeviceGuard g(ctx->device);
+    hipError_t e = hipStreamSynchronize(pick_stream(ctx, stream));
+    if (e != hipSuccess) rc = fail(ctx, QATTN_EHIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
+  }
+  qattn_run_destroy(run);
+  return rc;
+}
+
+// ---- mask check -------------------------------------------------------------------------------
+
+int qattn_debug_mask(qattn_ctx* ctx, int32_t L, int32_t mask, int32_t prefix, int32_t window,
+                     uint32_t* host_bits) {
+  if (!ctx) return fail(nullptr, QATTN_EINVAL, "ctx is NULL");
+  if (L > 0 && !host_bits) return fail(ctx, QATTN_EINVAL, "host_bits is NULL");
+  if (L < 0 || L > (1 << 20)) return fail(ctx, QATTN_EINVAL, "L=%d outside [0, 2^20]", L);
+  if (mask != QATTN_MASK_CAUSAL && mask != QATTN_MASK_PREFIX_LOCAL)
+    return fail(ctx, QATTN_EINVAL, "unknown mask kind %d", mask);
+  if (mask == QATTN_MASK_PREFIX_LOCAL && (prefix < 0 || window < 0 || (prefix == 0 && window == 0)))
+    return fail(ctx, QATTN_EINVAL, "bad prefix/window (%d, %d)", prefix, window);
+  if (L == 0) return QATTN_OK;
+  const int words = (L + 31) / 32;
+  const size_t bytes = (size_t)words * L * sizeof(uint32_t);
+  DeviceGuard g(ctx->device);
+  uint32_t* dev = nullptr;
+  HIP_TRY(ctx, hipMalloc(&dev, bytes));
+  const MaskSpec m{mask, mask == QATTN_MASK_PREFIX_LOCAL ? prefix : 0, mask == QATTN_MASK_PREFIX_LOCAL ? window : 0};
+  hipError_t e = hipMemsetAsync(dev, 0, bytes, ctx->stream);
+  if (e == hipSuccess) e = launch_debug_mask(L, m, dev, words, ctx->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(host_bits, dev, bytes, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  (void)hipFree(dev);
+  if (e != hipSuccess) return fail(ctx, QATTN_EHIP, "debug mask: %s", hipGetErrorString(e));
+  return QATTN_OK;
+}
+
+int qattn_plan_mask(int32_t L, int32_t mask, int32_t prefix, int32_t window, uint32_t* host_bits) {
+  if (L < 0 || L > (1 << 20)) return fail(nullptr, QATTN_EINVAL, "L=%d outside [0, 2^20]", L);
+  if (L > 0 && !host_bits) return fail(nullptr, QATTN_EINVAL, "host_bits is NULL");
+  if (mask != QATTN_MASK_CAUSAL && mask != QATTN_MASK_PREFIX_LOCAL)
+    return fail(nullptr, QATTN_EINVAL, "unknown mask kind %d", mask);
+  if (mask == QATTN_MASK_PREFIX_LOCAL && (prefix < 0 || window < 0 || (prefix == 0 && window == 0)))
+    return fail(nullptr, QATTN_EINVAL, "bad prefix/window (%d, %d)", prefix, window);
+  const MaskSpec m{mask, mask == QATTN_MASK_PREFIX_LOCAL ? prefix : 0, mask == QATTN_MASK_PREFIX_LOCAL ? window : 0};
+  const int words = (L + 31) / 32;
+  std::memset(host_bits, 0, (size_t)words * L * sizeof(uint32_t));
+  for (int q = 0; q < L; ++q) kept_keys_row(q, L, m, host_bits + (size_t)q * words, words);
+  return QATTN_OK;
+}
+
+// ---- producer + generator ---------------------------------------------------------------------
+
+int qattn_qk_norm_rope(qattn_ctx* ctx, void* x, int64_t row_stride, int64_t col0, int32_t heads,
+                       const int32_t* cu_seqlens, int32_t nseq, const float* weight, double eps,
+                       double theta, qattn_stream_t stream) {
+  if (!ctx || !x) return fail(ctx, QATTN_EINVAL, "ctx/x is NULL");
+  if (heads < 1 || col0 < 0 || row_stride < col0 + (int64_t)heads * kHeadDim)
+    return fail(ctx, QATTN_EINVAL, "bad heads/col0/row_stride (%d, %lld, %lld)", heads,
+                (long long)col0, (long long)row_stride);
+  if (!(eps >= 0.0) || !(theta > 0.0)) return fail(ctx, QATTN_EINVAL, "bad eps/theta");
+  int rc = validate_cu(ctx, cu_seqlens, nseq);
+  if (rc) return rc;
+  const int64_t T = cu_seqlens[nseq];
+  if (T == 0) return QATTN_OK;
+  int32_t maxlen = 0;
+  for (int32_t s = 0; s < nseq; ++s) maxlen = std::max(maxlen, cu_seqlens[s + 1] - cu_seqlens[s]);
+  // RoPE table exactly as model.ts:76-81: angle = pos * theta^(-i/64) in f64, cos/sin -> f32.
+  std::vector<float> table((size_t)maxlen * 128);
+  for (int32_t pos = 0; pos < maxlen; ++pos)
+    for (int i = 0; i < 64; ++i) {
+      const double angle = (double)pos * std::pow(theta, -(double)i / 64.0);
+      table[(size_t)pos * 64 + i] = (float)std::cos(angle);
+      table[(size_t)maxlen * 64 + (size_t)pos * 64 + i] = (float)std::sin(angle);
+    }
+  DeviceGuard g(ctx->device);
+  hipStream_t st = pick_stream(ctx, stream);
+  float* tab_dev = nullptr;
+  int32_t* cu_dev = nullptr;
+  HIP_TRY(ctx, hipMalloc(&tab_dev, table.size() * sizeof(float)));
+  hipError_t e = hipMalloc(&cu_dev, sizeof(int32_t) * (nseq + 1));
+  if (e == hipSuccess) e = hipMemcpyAsync(tab_dev, table.data(), table.size() * sizeof(float), hipMemcpyHostToDevice, st);
+  if (e == hipSuccess) e = hipMemcpyAsync(cu_dev, cu_seqlens, sizeof(int32_t) * (nseq + 1), hipMemcpyHostToDevice, st);
+  if (e == hipSuccess)
+    e = launch_qk_norm_rope(static_cast<half_t*>(x), row_stride, col0, heads, cu_dev, nseq, T, weight,
+                            eps, tab_dev, tab_dev + (size_t)maxlen * 64, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  (void)hipFree(tab_dev);
+  if (cu_dev) (void)hipFree(cu_dev);
+  if (e != hipSuccess) return fail(ctx, QATTN_EHIP, "qk_norm_rope: %s", hipGetErrorString(e));
+  return QATTN_OK;
+}
+
+int qattn_fill_normal(qattn_ctx* ctx, void* dst, int64_t rows, int64_t row_elems,
+                      int64_t row_stride, uint64_t seed, qattn_stream_t stream) {
+  if (!ctx || !dst) return fail(ctx, QATTN_EINVAL, "ctx/dst is NULL");
+  if (rows < 0 || row_elems < 0 || row_stride < row_elems)
+    return fail(ctx, QATTN_EINVAL, "bad rows/row_elems/row_stride");
+  DeviceGuard g(ctx->device);
+  HIP_TRY(ctx, launch_fill_normal(static_cast<half_t*>(dst), rows, row_elems, row_stride, seed,
+                                  pick_stream(ctx, stream)));
+  return QATTN_OK;
+}
+
+int qattn_gen_qkv(qattn_ctx* ctx, uint32_t config, uint32_t layer, const int32_t* cu_seqlens,
+                  int32_t nseq, void* q, int64_t q_row_stride, void* k, int64_t k_row_stride,
+                  void* v, int64_t v_row_stride, qattn_stream_t stream) {
+  if (!ctx || !q || !k || !v) return fail(ctx, QATTN_EINVAL, "NULL argument");
+  int rc = validate_cu(ctx, cu_seqlens, nseq);
+  if (rc) return rc;
+  if (q_row_stride < 2048 || k_row_stride < 1024 || v_row_stride < 1024)
+    return fail(ctx, QATTN_EINVAL, "row strides too small");
+  const int64_t T = cu_seqlens[nseq];
+  const uint64_t base = 0x51574E3300000000ULL | ((uint64_t)(config & 0xff) << 16) | ((uint64_t)(layer & 0xff) << 8);
+  rc = qattn_fill_normal(ctx, q, T, 2048, q_row_stride, base | 0, stream);
+  if (!rc) rc = qattn_fill_normal(ctx, k, T, 1024, k_row_stride, base | 1, stream);
+  if (!rc) rc = qattn_fill_normal(ctx, v, T, 1024, v_row_stride, base | 2, stream);
+  if (!rc) rc = qattn_qk_norm_rope(ctx, q, q_row_stride, 0, 16, cu_seqlens, nseq, nullptr, 1e-6, 1e6, stream);
+  if (!rc) rc = qattn_qk_norm_rope(ctx, k, k_row_stride, 0, 8, cu_seqlens, nseq, nullptr, 1e-6, 1e6, stream);
+  return rc;
+}
+
+// ---- timing -------------------------------------------------------------------------------------
+
+int qattn_event_create(qattn_ctx* ctx, qattn_event_t* ev) {
+  if (!ctx || !ev) return fail(ctx, QATTN_EINVAL, "NULL argument");
+  DeviceGuard g(ctx->device);
+  hipEvent_t e = nullptr;
+  HIP_TRY(ctx, hipEventCreate(&e));
+  *ev = e;
+  return QATTN_OK;
+}
+
+int qattn_event_record(qattn_event_t ev, qattn_stream_t stream) {
+  if (!ev) return fail(nullptr, QATTN_EINVAL, "event is NULL");
+  HIP_TRY(nullptr, hipEventRecord(reinterpret_cast<hipEvent_t>(ev), reinterpret_cast<hipStream_t>(stream)));
+  return QATTN_OK;
+}
+
+int qattn_event_elapsed_ms(qattn_event_t a, qattn_event_t b, float* ms) {
+  if (!a || !b || !ms) return fail(nullptr, QATTN_EINVAL, "NULL argument");
+  HIP_TRY(nullptr, hipEventSynchronize(reinterpret_cast<hipEvent_t>(b)));
+  HIP_TRY(nullptr, hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(a), reinterpret_cast<hipEvent_t>(b)));
+  return QATTN_OK;
+}
+
+int qattn_event_destroy(qattn_event_t ev) {
+  if (!ev) return QATTN_OK;
+  HIP_TRY(nullptr, hipEventDestroy(reinterpret_cast<hipEvent_t>(ev)));
+  return QATTN_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,129 @@
+// attn_common.h -- geometry, mask predicate and key-tile iterator shared by the attention
+// kernel, the debug-mask kernel and the host planner.  One definition of "which keys does a
+// query see" for every consumer, so the bit-exact mask check exercises the kernel's own code.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qattn {
+
+constexpr int kHeadDim = 128;  // model.ts:18-23 (Q_WIDTH 2048 / 16 heads)
+constexpr int kQHeads = 16;
+constexpr int kKVHeads = 8;
+constexpr int kGroup = kQHeads / kKVHeads;  // ops.ts:196 kv_head = q_head / 2
+
+constexpr int kBlockQ = 64;   // query positions per work item (x 2 heads of one KV group)
+constexpr int kTileK = 64;    // keys per LDS tile
+constexpr int kWaveQ = 32;    // query positions per wavefront (one 32-row MFMA tile)
+constexpr int kWaves = kGroup * kBlockQ / kWaveQ;  // 4
+constexpr int kThreads = kWaves * 64;
+
+struct MaskSpec {
+  int kind;    // 0 causal, 1 prefix + local window
+  int prefix;  // reference 176
+  int window;  // reference 432
+};
+
+// Reference predicate ops.ts:205-206,220, clamps included:
+//   q < S && k <= q && k < S && (k < min(S,prefix) || k + min(S,window) > q)
+// (the causal kind drops the last conjunct).
+__host__ __device__ inline bool retained(int q, int k, int S, const MaskSpec& m) {
+  if (!(q < S && k <= q && k < S)) return false;
+  if (m.kind == 0) return true;
+  const int ps = S < m.prefix ? S : m.prefix;
+  const int ws = S < m.window ? S : m.window;
+  return k < ps || k + ws > q;
+}
+
+// Key tiles that query rows [qa, qb] (0 <= qa <= qb < S) of one sequence must visit: at most two
+// half-open ranges of tile indices.  Causal: keys <= qb.  Prefix/local: keys < min(S,prefix)
+// plus keys >= qa - min(S,window) + 1; every key outside both is masked for every row in
+// [qa, qb] (k + ws > q with q >= qa needs k >= qa - ws + 1), so skipping it is exact.
+struct TileRanges {
+  int b0, e0, b1, e1;
+  __host__ __device__ int count() const { return (e0 - b0) + (e1 - b1); }
+  __host__ __device__ int at(int i) const { return i < e0 - b0 ? b0 + i : b1 + (i - (e0 - b0)); }
+};
+
+__host__ __device__ inline TileRanges key_tiles(int qa, int qb, int S, const MaskSpec& m) {
+  TileRanges r;
+  const int last = qb / kTileK;
+  r.b0 = 0;
+  r.e0 = last + 1;
+  r.b1 = 0;
+  r.e1 = 0;
+  if (m.kind == 0) return r;
+  const int ps = S < m.prefix ? S : m.prefix;
+  const int ws = S < m.window ? S : m.window;
+  int pe = (ps + kTileK - 1) / kTileK;
+  if (pe > last + 1) pe = last + 1;
+  int wstart = qa - ws + 1;
+  if (wstart < 0) wstart = 0;
+  const int wb = wstart / kTileK;
+  if (wb > pe) {
+    r.e0 = pe;
+    r.b1 = wb;
+    r.e1 = last + 1;
+  }
+  return r;
+}
+
+// Does key tile [kb, kb+kTileK) hold any candidate key for rows [qa, qb]?  Conservative (may
+// answer true for a tile with no retained key; never false for one with a retained key).
+__host__ __device__ inline bool tile_any(int kb, int qa, int qb, int S, const MaskSpec& m) {
+  if (kb > qb) return false;
+  if (m.kind == 0) return true;
+  const int ps = S < m.prefix ? S : m.prefix;
+  const int ws = S < m.window ? S : m.window;
+  const int ke = kb + kTileK - 1;
+  return kb < ps || ke >= qa - ws + 1;
+}
+
+// Is every key of the tile retained for every row in [qa, qb]?  Then no element mask is needed.
+__host__ __device__ inline bool tile_full(int kb, int qa, int qb, int S, const MaskSpec& m) {
+  const int ke = kb + kTileK - 1;
+  if (ke > qa) return false;  // causal for the first row (ke <= qa < S also keeps keys in range)
+  if (m.kind == 0) return true;
+  const int ps = S < m.prefix ? S : m.prefix;
+  const int ws = S < m.window ? S : m.window;
+  return ke < ps || qb - kb < ws;
+}
+
+// Keys the attention kernel keeps for query row q of a sequence of length S, as a bitmask row
+// (word k/32, bit k%32; `row` pre-zeroed, `words` = ceil(S/32)).  Walks the kernel's own
+// iteration: the work item's tile ranges (key_tiles over its 64 rows), the wavefront's tile test
+// (tile_any over its 32 rows) and the element rule (tile_full, else retained).
+__host__ __device__ inline void kept_keys_row(int q, int S, const MaskSpec& m, uint32_t* row,
+                                              int words) {
+  const int blk_q0 = (q / kBlockQ) * kBlockQ;
+  const int blk_q1 = (S < blk_q0 + kBlockQ ? S : blk_q0 + kBlockQ) - 1;
+  const int wq0 = (q / kWaveQ) * kWaveQ;
+  const int wq1 = (S - 1 < wq0 + kWaveQ - 1) ? S - 1 : wq0 + kWaveQ - 1;
+  const TileRanges tiles = key_tiles(blk_q0, blk_q1, S, m);
+  for (int it = 0; it < tiles.count(); ++it) {
+    const int kb = tiles.at(it) * kTileK;
+    if (!tile_any(kb, wq0, wq1, S, m)) continue;
+    const bool full = tile_full(kb, wq0, wq1, S, m);
+    for (int wd = 0; wd < kTileK / 32; ++wd) {
+      uint32_t word = 0;
+      for (int b = 0; b < 32; ++b) {
+        const int key = kb + 32 * wd + b;
+        // Keys >= S are zero-filled in LDS and dropped by retained(); a full tile has
+        // every key <= its first row < S.
+        if (key < S && (full || retained(q, key, S, m))) word |= 1u << b;
+      }
+      const int wi = kb / 32 + wd;
+      if (wi < words) row[wi] = word;
+    }
+  }
+}
+
+// Work item of one launch: (sequence start token, length, query block, sequence<<4 | kv_head).
+struct WorkItem {
+  int seq_start;
+  int seq_len;
+  int q_block;
+  int seq_kvh;
+};
+
+}  // namespace qattn

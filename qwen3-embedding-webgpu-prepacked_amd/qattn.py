@@ -1,0 +1,311 @@
+"""ctypes binding of libqattn.so (C ABI: include/qattn.h) for Python hosts: the test suite and
+bench.py.  The product's own host is the Node engine in js/; this module mirrors the same
+operator interface (the reference's CausalAttentionKernel.createRun / encode,
+src/webgpu/ops.ts:327-345) so Python callers drive exactly the code Node drives.
+
+There is no fallback: if libqattn.so is missing or no gfx950 device is present, the calls raise.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO_DIR = os.path.dirname(PKG_DIR)
+LIB_PATH = os.path.join(PKG_DIR, "libqattn.so")
+HEADER_PATH = os.path.join(REPO_DIR, "include", "qattn.h")
+
+OK, EINVAL, EHIP, ENOMEM, ENODEV = 0, -1, -2, -3, -4
+MASK_CAUSAL, MASK_PREFIX_LOCAL = 0, 1
+HQ, HKV, HD = 16, 8, 128
+
+
+class QattnError(RuntimeError):
+    def __init__(self, code, message):
+        super().__init__(f"qattn error {code}: {message}")
+        self.code = code
+
+
+class RunDesc(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("o", ctypes.c_void_p),
+        ("q_row_stride", ctypes.c_int64), ("k_row_stride", ctypes.c_int64),
+        ("v_row_stride", ctypes.c_int64), ("o_row_stride", ctypes.c_int64),
+        ("v_offset", ctypes.c_int64),
+        ("cu_seqlens", ctypes.c_void_p), ("nseq", ctypes.c_int32),
+        ("mask", ctypes.c_int32), ("prefix", ctypes.c_int32), ("window", ctypes.c_int32),
+        ("o_last", ctypes.c_void_p),
+    ]
+
+
+class RunInfo(ctypes.Structure):
+    _fields_ = [
+        ("tokens", ctypes.c_int64), ("pairs", ctypes.c_int64), ("flops", ctypes.c_int64),
+        ("bytes", ctypes.c_int64), ("work_items", ctypes.c_int32),
+        ("block_queries", ctypes.c_int32), ("tile_pairs", ctypes.c_int64),
+    ]
+
+    def as_dict(self):
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+def build():
+    """Compile libqattn.so for gfx950 with the package Makefile."""
+    subprocess.run(["make", "-s", "-C", PKG_DIR, "lib"], check=True)
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise QattnError(ENODEV, f"{LIB_PATH} is not built (run __graft_entry__.build())")
+    L = ctypes.CDLL(LIB_PATH)
+    vp, i32, i64, sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t
+    pvp = ctypes.POINTER(ctypes.c_void_p)
+    sigs = {
+        "qattn_abi_version": (ctypes.c_int, []),
+        "qattn_create": (ctypes.c_int, [ctypes.c_int, pvp]),
+        "qattn_destroy": (None, [vp]),
+        "qattn_last_error": (ctypes.c_char_p, [vp]),
+        "qattn_stream": (vp, [vp]),
+        "qattn_synchronize": (ctypes.c_int, [vp]),
+        "qattn_device_name": (ctypes.c_int, [vp, ctypes.c_char_p, sz, ctypes.POINTER(ctypes.c_int)]),
+        "qattn_buffer_alloc": (ctypes.c_int, [vp, sz, pvp]),
+        "qattn_buffer_free": (ctypes.c_int, [vp, vp]),
+        "qattn_buffer_write": (ctypes.c_int, [vp, vp, sz, vp, sz]),
+        "qattn_buffer_read": (ctypes.c_int, [vp, vp, sz, vp, sz]),
+        "qattn_buffer_fill_u16": (ctypes.c_int, [vp, vp, ctypes.c_uint16, sz]),
+        "qattn_run_create": (ctypes.c_int, [vp, ctypes.POINTER(RunDesc), pvp]),
+        "qattn_run_encode": (ctypes.c_int, [vp, vp]),
+        "qattn_run_rebind": (ctypes.c_int, [vp, vp, vp, vp, vp, vp]),
+        "qattn_run_destroy": (None, [vp]),
+        "qattn_run_get_info": (ctypes.c_int, [vp, ctypes.POINTER(RunInfo)]),
+        "qattn_plan_describe": (ctypes.c_int, [ctypes.POINTER(RunDesc), vp, i32,
+                                               ctypes.POINTER(i32), ctypes.POINTER(RunInfo)]),
+        "qattn_prefill": (ctypes.c_int, [vp, ctypes.POINTER(RunDesc), vp]),
+        "qattn_debug_mask": (ctypes.c_int, [vp, i32, i32, i32, i32, vp]),
+        "qattn_plan_mask": (ctypes.c_int, [i32, i32, i32, i32, vp]),
+        "qattn_qk_norm_rope": (ctypes.c_int, [vp, vp, i64, i64, i32, vp, i32, vp,
+                                              ctypes.c_double, ctypes.c_double, vp]),
+        "qattn_fill_normal": (ctypes.c_int, [vp, vp, i64, i64, i64, ctypes.c_uint64, vp]),
+        "qattn_gen_qkv": (ctypes.c_int, [vp, ctypes.c_uint32, ctypes.c_uint32, vp, i32,
+                                         vp, i64, vp, i64, vp, i64, vp]),
+        "qattn_event_create": (ctypes.c_int, [vp, pvp]),
+        "qattn_event_record": (ctypes.c_int, [vp, vp]),
+        "qattn_event_elapsed_ms": (ctypes.c_int, [vp, vp, ctypes.POINTER(ctypes.c_float)]),
+        "qattn_event_destroy": (ctypes.c_int, [vp]),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def _check(rc, ctx=None):
+    if rc != OK:
+        msg = lib().qattn_last_error(ctx)
+        raise QattnError(rc, msg.decode() if msg else "")
+
+
+def _np_ptr(a):
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def make_desc(q, k, v, o, cu_seqlens, mask=MASK_PREFIX_LOCAL, prefix=176, window=432,
+              q_row_stride=HQ * HD, k_row_stride=HKV * HD, v_row_stride=HKV * HD,
+              o_row_stride=HQ * HD, v_offset=0, o_last=None):
+    """Build a qattn_run_desc.  q/k/v/o/o_last are device addresses (int).  The returned desc
+    keeps a reference to its cu_seqlens array."""
+    cu = np.ascontiguousarray(cu_seqlens, dtype=np.int32)
+    d = RunDesc(q, k, v, o, q_row_stride, k_row_stride, v_row_stride, o_row_stride, v_offset,
+                cu.ctypes.data, len(cu) - 1, mask, prefix, window, o_last)
+    d._cu = cu
+    return d
+
+
+def plan_describe(desc):
+    """Host-only planner: (work items int32[n,4] in launch order, RunInfo)."""
+    n = ctypes.c_int32(0)
+    info = RunInfo()
+    _check(lib().qattn_plan_describe(ctypes.byref(desc), None, 0, ctypes.byref(n), ctypes.byref(info)))
+    items = np.zeros((n.value, 4), dtype=np.int32)
+    if n.value:
+        _check(lib().qattn_plan_describe(ctypes.byref(desc), _np_ptr(items), n.value,
+                                         ctypes.byref(n), None))
+    return items, info
+
+
+def plan_mask(L, mask=MASK_PREFIX_LOCAL, prefix=176, window=432):
+    """Host run of the kernel's key iteration: uint32 [L, ceil(L/32)] bitmask."""
+    out = np.zeros((L, (L + 31) // 32), dtype=np.uint32)
+    _check(lib().qattn_plan_mask(L, mask, prefix, window, _np_ptr(out) if L else None))
+    return out
+
+
+class Buffer:
+    """Device allocation owned by a Context."""
+
+    def __init__(self, ctx, nbytes):
+        self.ctx = ctx
+        self.nbytes = int(nbytes)
+        p = ctypes.c_void_p()
+        _check(lib().qattn_buffer_alloc(ctx.handle, self.nbytes, ctypes.byref(p)), ctx.handle)
+        self.ptr = p.value
+
+    def write(self, array, offset=0):
+        a = np.ascontiguousarray(array)
+        assert offset + a.nbytes <= self.nbytes
+        _check(lib().qattn_buffer_write(self.ctx.handle, self.ptr, offset, _np_ptr(a), a.nbytes),
+               self.ctx.handle)
+
+    def read(self, dtype, shape, offset=0):
+        out = np.empty(shape, dtype=dtype)
+        assert offset + out.nbytes <= self.nbytes
+        _check(lib().qattn_buffer_read(self.ctx.handle, self.ptr, offset, _np_ptr(out), out.nbytes),
+               self.ctx.handle)
+        return out
+
+    def fill_u16(self, value, count=None):
+        count = self.nbytes // 2 if count is None else count
+        _check(lib().qattn_buffer_fill_u16(self.ctx.handle, self.ptr, value, count), self.ctx.handle)
+
+    def free(self):
+        if self.ptr:
+            _check(lib().qattn_buffer_free(self.ctx.handle, self.ptr), self.ctx.handle)
+            self.ptr = None
+
+
+class Run:
+    """A planned attention launch (reference: AttentionRun from createRun, ops.ts:318-343)."""
+
+    def __init__(self, ctx, desc):
+        self.ctx = ctx
+        self.desc = desc
+        h = ctypes.c_void_p()
+        _check(lib().qattn_run_create(ctx.handle, ctypes.byref(desc), ctypes.byref(h)), ctx.handle)
+        self.handle = h.value
+
+    def encode(self, stream=None):
+        _check(lib().qattn_run_encode(self.handle, stream), self.ctx.handle)
+
+    def rebind(self, q, k, v, o, o_last=None):
+        _check(lib().qattn_run_rebind(self.handle, q, k, v, o, o_last), self.ctx.handle)
+
+    def info(self):
+        i = RunInfo()
+        _check(lib().qattn_run_get_info(self.handle, ctypes.byref(i)), self.ctx.handle)
+        return i
+
+    def destroy(self):
+        if self.handle:
+            lib().qattn_run_destroy(self.handle)
+            self.handle = None
+
+
+class Event:
+    def __init__(self, ctx):
+        self.ctx = ctx
+        e = ctypes.c_void_p()
+        _check(lib().qattn_event_create(ctx.handle, ctypes.byref(e)), ctx.handle)
+        self.handle = e.value
+
+    def record(self, stream=None):
+        _check(lib().qattn_event_record(self.handle, stream if stream else self.ctx.stream))
+
+    def elapsed_ms(self, later):
+        ms = ctypes.c_float()
+        _check(lib().qattn_event_elapsed_ms(self.handle, later.handle, ctypes.byref(ms)))
+        return ms.value
+
+    def destroy(self):
+        if self.handle:
+            lib().qattn_event_destroy(self.handle)
+            self.handle = None
+
+
+class Context:
+    """Device context (reference: requestWebGPUDevice, src/webgpu/device.ts:6-24)."""
+
+    def __init__(self, device=0):
+        h = ctypes.c_void_p()
+        _check(lib().qattn_create(device, ctypes.byref(h)))
+        self.handle = h.value
+        self.stream = lib().qattn_stream(self.handle)
+
+    def close(self):
+        if self.handle:
+            lib().qattn_destroy(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def device_name(self):
+        buf = ctypes.create_string_buffer(256)
+        cu = ctypes.c_int()
+        _check(lib().qattn_device_name(self.handle, buf, 256, ctypes.byref(cu)), self.handle)
+        return buf.value.decode(), cu.value
+
+    def synchronize(self):
+        _check(lib().qattn_synchronize(self.handle), self.handle)
+
+    def alloc(self, nbytes):
+        return Buffer(self, nbytes)
+
+    def upload(self, array):
+        a = np.ascontiguousarray(array)
+        b = Buffer(self, max(a.nbytes, 16))
+        b.write(a)
+        return b
+
+    def run(self, desc):
+        return Run(self, desc)
+
+    def prefill(self, desc, stream=None):
+        _check(lib().qattn_prefill(self.handle, ctypes.byref(desc), stream), self.handle)
+
+    def debug_mask(self, L, mask=MASK_PREFIX_LOCAL, prefix=176, window=432):
+        words = (L + 31) // 32
+        out = np.zeros((L, words), dtype=np.uint32)
+        _check(lib().qattn_debug_mask(self.handle, L, mask, prefix, window,
+                                      _np_ptr(out) if L else None), self.handle)
+        return out
+
+    def qk_norm_rope(self, x_ptr, row_stride, col0, heads, cu_seqlens, weight_ptr=None,
+                     eps=1e-6, theta=1e6, stream=None):
+        cu = np.ascontiguousarray(cu_seqlens, dtype=np.int32)
+        _check(lib().qattn_qk_norm_rope(self.handle, x_ptr, row_stride, col0, heads, _np_ptr(cu),
+                                        len(cu) - 1, weight_ptr, eps, theta, stream), self.handle)
+
+    def fill_normal(self, ptr, rows, row_elems, row_stride, seed, stream=None):
+        _check(lib().qattn_fill_normal(self.handle, ptr, rows, row_elems, row_stride, seed, stream),
+               self.handle)
+
+    def gen_qkv(self, config, layer, cu_seqlens, q_ptr, k_ptr, v_ptr, q_row_stride=HQ * HD,
+                k_row_stride=HKV * HD, v_row_stride=HKV * HD, stream=None):
+        cu = np.ascontiguousarray(cu_seqlens, dtype=np.int32)
+        _check(lib().qattn_gen_qkv(self.handle, config, layer, _np_ptr(cu), len(cu) - 1,
+                                   q_ptr, q_row_stride, k_ptr, k_row_stride, v_ptr, v_row_stride,
+                                   stream), self.handle)
+
+    def event(self):
+        return Event(self)
+
+
+def header_symbols(path=HEADER_PATH):
+    """Function names declared in include/qattn.h."""
+    import re
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(qattn_[a-z0-9_]+)\s*\(", text)))

@@ -1,0 +1,150 @@
+"""CPU checks of the C ABI (include/qattn.h / libqattn.so) that need no GPU: the library loads
+and exports every declared symbol, the host planner's work list and figures, argument
+validation, and the kernel's key-tile iteration (compiled for the host from the same
+attn_common.h) against the oracle's mask, bit for bit.
+"""
+import ctypes
+import subprocess
+
+import numpy as np
+import pytest
+
+FAKE = 0x100000  # aligned, non-NULL stand-in device addresses for host-only planning
+
+
+def _desc(qattn, lengths, mask=1, P=176, W=432, **kw):
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    return qattn.make_desc(FAKE, FAKE, FAKE, FAKE, cu, mask, P, W, **kw)
+
+
+def test_library_exports_every_declared_symbol(qattn):
+    declared = qattn.header_symbols()
+    assert len(declared) >= 25
+    out = subprocess.run(["nm", "-D", "--defined-only", qattn.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    missing = [s for s in declared if s not in exported]
+    assert not missing, missing
+    lib = qattn.lib()
+    for s in declared:
+        assert getattr(lib, s) is not None
+
+
+def test_abi_version(qattn):
+    assert qattn.lib().qattn_abi_version() == 1
+
+
+def test_create_without_gpu_fails_cleanly(qattn):
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    with pytest.raises(qattn.QattnError) as e:
+        qattn.Context(0)
+    assert e.value.code in (qattn.ENODEV, qattn.EHIP)
+    assert qattn.lib().qattn_last_error(None)
+
+
+@pytest.mark.parametrize("lengths,mask", [([50], 1), ([500] * 16, 1), ([5000], 1), ([1500], 1),
+                                          ([10, 150, 64, 65, 1], 0), ([5000] * 4, 1)])
+def test_planner_covers_every_block_once_heaviest_first(qattn, oracle, lengths, mask):
+    items, info = qattn.plan_describe(_desc(qattn, lengths, mask))
+    want = {(int(np.sum(lengths[:s])), L, qb, (s << 4) | g)
+            for s, L in enumerate(lengths) for qb in range((L + 63) // 64) for g in range(8)}
+    got = [tuple(int(x) for x in it) for it in items]
+    assert len(got) == len(want) == info.work_items
+    assert set(got) == want
+    # heaviest first: the number of key tiles visited never increases along the list
+    ntiles = [len(_tiles(it[2], it[1], mask)) for it in got]
+    assert all(a >= b for a, b in zip(ntiles, ntiles[1:]))
+    # figures
+    pairs = sum(oracle.mask_pairs(L, mask) for L in lengths)
+    assert info.tokens == sum(lengths)
+    assert info.pairs == pairs
+    assert info.flops == 8192 * pairs
+    assert info.bytes == 12288 * sum(lengths)
+    assert info.tile_pairs >= pairs
+
+
+def _tiles(qb, L, mask, P=176, W=432):
+    q0, q1 = qb * 64, min(L, qb * 64 + 64) - 1
+    last = q1 // 64
+    if mask == 0:
+        return list(range(last + 1))
+    ps, ws = min(L, P), min(L, W)
+    keep = set(range(min(last + 1, (ps + 63) // 64)))
+    keep |= set(range(max(0, q0 - ws + 1) // 64, last + 1))
+    return sorted(keep)
+
+
+def test_planner_sparse_tile_count_closed_form(qattn):
+    # 1 x 5000, prefix 176 / window 432, 64-key tiles: block qb (rows 64qb..64qb+63) visits the
+    # 3 prefix tiles plus tiles floor((64qb-431)/64) .. qb.
+    items, info = qattn.plan_describe(_desc(qattn, [5000]))
+    assert info.work_items == 79 * 8
+    assert info.pairs == 2855472
+    # every block past the prefix region visits at most 3 + 8 + 1 tiles
+    assert max(len(_tiles(qb, 5000, 1)) for qb in range(79)) <= 12
+
+
+def test_planner_o_last_bytes(qattn):
+    _, info = qattn.plan_describe(_desc(qattn, [5000] * 4, o_last=FAKE))
+    assert info.bytes == 12288 * 20000 + 4096 * 4
+
+
+@pytest.mark.parametrize("bad,needle", [
+    (dict(lengths=[5, 3], cu=[0, 5, 4]), "non-decreasing"),
+    (dict(lengths=[5], cu=[1, 6]), "cu_seqlens[0]"),
+    (dict(lengths=[5], q_row_stride=2052), "multiples of 8"),
+    (dict(lengths=[5], k_row_stride=512), "too small"),
+    (dict(lengths=[5], v_offset=3), "multiples of 8"),
+    (dict(lengths=[5], mask=7), "unknown mask"),
+    (dict(lengths=[5], P=0, W=0), "both 0"),
+    (dict(lengths=[5], P=-1), ">= 0"),
+    (dict(lengths=[5], misalign=True), "aligned"),
+])
+def test_validation_rejects_before_launch(qattn, bad, needle):
+    lengths = bad.pop("lengths")
+    cu = bad.pop("cu", None)
+    misalign = bad.pop("misalign", False)
+    d = _desc(qattn, lengths, mask=bad.pop("mask", 1), P=bad.pop("P", 176), W=bad.pop("W", 432), **bad)
+    if cu is not None:
+        d._cu = np.asarray(cu, np.int32)
+        d.cu_seqlens = d._cu.ctypes.data
+        d.nseq = len(cu) - 1
+    if misalign:
+        d.k = FAKE + 2
+    with pytest.raises(qattn.QattnError) as e:
+        qattn.plan_describe(d)
+    assert e.value.code == qattn.EINVAL
+    assert needle in str(e.value)
+
+
+def test_validation_nseq_zero_and_null(qattn):
+    d = _desc(qattn, [5])
+    d.nseq = 0
+    with pytest.raises(qattn.QattnError):
+        qattn.plan_describe(d)
+    d = _desc(qattn, [5])
+    d.q = None
+    with pytest.raises(qattn.QattnError):
+        qattn.plan_describe(d)
+
+
+def test_empty_sequences_are_skipped(qattn):
+    items, info = qattn.plan_describe(_desc(qattn, [0, 7, 0, 0, 70]))
+    assert info.tokens == 77 and info.work_items == 8 * (1 + 2)
+    assert {int(i[0]) for i in items} == {0, 7}
+
+
+@pytest.mark.parametrize("L", [1, 2, 16, 31, 32, 33, 63, 64, 65, 127, 175, 176, 177, 431, 432, 433,
+                               500, 607, 608, 609, 700, 1500, 5000])
+def test_kernel_key_iteration_matches_reference_mask(qattn, oracle, L):
+    got = qattn.plan_mask(L)
+    want = oracle.mask_bits(L)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("L,mask,P,W", [(300, 0, 0, 0), (129, 1, 7, 50), (200, 1, 0, 33), (200, 1, 64, 1),
+                                         (333, 1, 1, 200), (1000, 1, 300, 64)])
+def test_kernel_key_iteration_other_masks(qattn, oracle, L, mask, P, W):
+    assert np.array_equal(qattn.plan_mask(L, mask, P, W), oracle.mask_bits(L, mask, P, W))
