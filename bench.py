@@ -1,0 +1,277 @@
+#!/usr/bin/env python3
+"""Prefill-attention throughput of libqattn.so on one MI355X (BASELINE.json metric).
+
+One step = the hot path over the two workloads the metric is quoted on, each for all 28 layers
+of independent seeded Q/K/V resident in HBM:
+  * 16 x 500 tokens, full causal      (BASELINE config 2)
+  * 1 x 5000 tokens, 176-prefix + 432-local sparse causal (the metric's sparse row)
+Every launch is one layer's attention through the C ABI (qattn_run_encode), exactly what the
+Node engine issues.  Timing: HIP events on the launch stream around exactly K steps, with a
+device synchronize on both sides.  A second pass brackets every launch with its own events to
+get the kernel's average duration for the roofline figure.
+
+cpu_baseline: the reference's tiled algorithm restated on the CPU (oracle/, f16-faithful, the
+"port"), timed on a bounded sample of the same workload on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload both|full|sparse|cfg3|cfg4]
+"""
+import argparse
+import importlib.util
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(REPO, "qwen3-embedding-webgpu-prepacked_amd")
+LAYERS = 28
+PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16/bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+WORKLOADS = {
+    # name: (config id for seeds, lengths, mask kind, description)
+    "full": (2, [500] * 16, 0, "16x500 full causal"),
+    "sparse": (5, [5000], 1, "1x5000 sparse (176 prefix + 432 window)"),
+    "cfg3": (3, [1500], 1, "1x1500 sparse (176 prefix + 432 window)"),
+    "cfg4": (4, [5000] * 4, 1, "4x5000 sparse (176 prefix + 432 window) + last rows"),
+}
+SETS = {"both": ["full", "sparse"], "full": ["full"], "sparse": ["sparse"], "cfg3": ["cfg3"],
+        "cfg4": ["cfg4"]}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def load_binding():
+    spec = importlib.util.spec_from_file_location("qattn", os.path.join(PKG, "qattn.py"))
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["qattn"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+class Workload:
+    """28 layers of one packing, resident in HBM, with one planned run per layer."""
+
+    def __init__(self, ctx, q, name):
+        self.name = name
+        cfg, lengths, mask, desc = WORKLOADS[name]
+        self.desc_text = desc
+        self.lengths = lengths
+        self.cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+        T = int(self.cu[-1])
+        self.tokens = T
+        nseq = len(lengths)
+        self.bufs, self.runs = [], []
+        for layer in range(LAYERS):
+            bq, bk, bv = ctx.alloc(T * 4096), ctx.alloc(T * 2048), ctx.alloc(T * 2048)
+            bo = ctx.alloc(T * 4096)
+            bl = ctx.alloc(nseq * 4096) if name == "cfg4" else None
+            ctx.gen_qkv(cfg, layer, self.cu, bq.ptr, bk.ptr, bv.ptr)
+            d = q.make_desc(bq.ptr, bk.ptr, bv.ptr, bo.ptr, self.cu, mask=mask,
+                            o_last=bl.ptr if bl else None)
+            self.runs.append(ctx.run(d))
+            self.bufs += [b for b in (bq, bk, bv, bo, bl) if b]
+        ctx.synchronize()
+        self.info = self.runs[0].info()
+
+    def encode_all(self):
+        for r in self.runs:
+            r.encode()
+
+    def free(self):
+        for r in self.runs:
+            r.destroy()
+        for b in self.bufs:
+            b.free()
+
+
+def cpu_baseline(selected):
+    """Time the oracle's f16-faithful restatement of the reference's tiled kernel on a bounded
+    sample of each workload's layer, scale to 28 layers, return tokens/s over the same step."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle
+    threads = oracle.get_threads()
+    total_s = 0.0
+    samples = []
+    for name in selected:
+        cfg, lengths, mask, _ = WORKLOADS[name]
+        if len(lengths) > 1:
+            # whole sequences: 4 of the batch (all equal length), scaled by nseq / 4
+            k = min(4, len(lengths))
+            sub = lengths[:k]
+            cu = np.concatenate([[0], np.cumsum(sub)]).astype(np.int32)
+            qh, kh, vh = oracle.gen_qkv(cfg, 0, cu)
+            t0 = time.perf_counter()
+            oracle.attention_tiled16(qh, kh, vh, cu, kind=mask)
+            dt = time.perf_counter() - t0
+            layer_s = dt * len(lengths) / k
+            samples.append(f"{name}: {k} of {len(lengths)} sequences of layer 0")
+        else:
+            # every 4th 16-query tile of the single sequence, scaled by the tile count ratio
+            L = lengths[0]
+            cu = np.array([0, L], dtype=np.int32)
+            qh, kh, vh = oracle.gen_qkv(cfg, 0, cu)
+            ntiles = (L + 15) // 16
+            step = 4
+            done = len(range(0, ntiles, step))
+            t0 = time.perf_counter()
+            oracle.attention_tiled16_tiles(qh, kh, vh, cu, 0, 0, ntiles, step, kind=mask)
+            dt = time.perf_counter() - t0
+            layer_s = dt * ntiles / done
+            samples.append(f"{name}: every {step}th 16-query tile ({done} of {ntiles}) of layer 0")
+        log(f"cpu baseline {name}: sample {dt:.2f} s -> {layer_s:.2f} s per layer")
+        total_s += layer_s * LAYERS
+    tokens = sum(sum(WORKLOADS[n][1]) for n in selected) * LAYERS
+    return {
+        "value": tokens / total_s,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": "; ".join(samples) + f"; x{LAYERS} layers; f16-faithful restatement of the "
+                  "reference's 16x16 tiled WGSL kernel (oracle/oracle.c, OpenMP)",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", choices=sorted(SETS), default="both")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (each GPU box has one "
+              "MI355X). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    q = load_binding()
+    ctx = q.Context(0)
+    dev, cus = ctx.device_name()
+    log(f"device {dev} ({cus} CUs)")
+    selected = SETS[args.workload]
+    wls = [Workload(ctx, q, n) for n in selected]
+    for w in wls:
+        i = w.info
+        log(f"{w.name}: {w.desc_text}: tokens {i.tokens}, pairs {i.pairs}, work items {i.work_items}, "
+            f"flops/launch {i.flops:.4e}, bytes/launch {i.bytes:.4e}, tile waste {i.tile_pairs / i.pairs:.3f}")
+
+    def step():
+        for w in wls:
+            w.encode_all()
+
+    for _ in range(args.warmup):
+        step()
+    ctx.synchronize()
+
+    # ---- timed region: exactly K steps ----
+    e0, e1 = ctx.event(), ctx.event()
+    ctx.synchronize()
+    t_host = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    ctx.synchronize()
+    host_ms = (time.perf_counter() - t_host) * 1e3
+    region_ms = e0.elapsed_ms(e1)
+    ms_per_step = region_ms / args.steps
+    log(f"timed {args.steps} steps: {region_ms:.3f} ms on device events ({host_ms:.3f} ms host)")
+
+    # ---- per-launch kernel durations (separate pass, same launches) ----
+    reps = max(3, min(args.steps, 10))
+    per = {w.name: [] for w in wls}
+    evs = [(ctx.event(), ctx.event()) for _ in range(LAYERS)]
+    for _ in range(reps):
+        for w in wls:
+            for r, (a, b) in zip(w.runs, evs):
+                a.record()
+                r.encode()
+                b.record()
+            ctx.synchronize()
+            per[w.name] += [a.elapsed_ms(b) for a, b in evs]
+    for a, b in evs:
+        a.destroy()
+        b.destroy()
+
+    tokens_per_step = sum(w.tokens for w in wls) * LAYERS
+    value = tokens_per_step / (ms_per_step / 1e3)
+    total_flops = sum(w.info.flops for w in wls) * LAYERS
+    total_bytes = sum(w.info.bytes for w in wls) * LAYERS
+    kern_ms_step = sum(np.mean(per[w.name]) * LAYERS for w in wls)
+    breakdown = {}
+    for w in wls:
+        avg = float(np.mean(per[w.name]))
+        breakdown[w.name] = {
+            "workload": w.desc_text,
+            "kernel_avg_us": round(avg * 1e3, 3),
+            "tokens_per_s": round(w.tokens / (avg / 1e3), 1),
+            "tflops": round(w.info.flops / (avg / 1e3) / 1e12, 2),
+            "mfma_frac": round(w.info.flops / (avg / 1e3) / 1e12 / PEAK_FP16_TFLOPS, 4),
+            "gbs": round(w.info.bytes / (avg / 1e3) / 1e9, 1),
+            "hbm_frac": round(w.info.bytes / (avg / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
+        }
+        log(f"{w.name}: kernel avg {avg * 1e3:.2f} us, {breakdown[w.name]}")
+    achieved = total_flops / (kern_ms_step / 1e3) / 1e12
+
+    traffic = None
+    tpath = os.path.join(REPO, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        try:
+            traffic = json.load(open(tpath)).get(args.workload)
+        except (ValueError, OSError):
+            traffic = None
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        try:
+            cpu = cpu_baseline(selected)
+        except Exception as e:  # the baseline is reported, never the measured path
+            log(f"cpu baseline failed: {e}")
+
+    out = {
+        "metric": "prefill-attn tokens/s/GPU at 16x500 full & 1x5000 sparse; % fp16 MFMA peak",
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded N(0,1) Q/K/V, QK RMSNorm + RoPE theta 1e6, generated on device)",
+        "config": {
+            "workload": " + ".join(w.desc_text for w in wls) + f", {LAYERS} layers each, "
+                        "16 q heads / 8 kv heads, head_dim 128",
+            "layers": LAYERS,
+            "tokens_per_step": tokens_per_step,
+            "launches_per_step": LAYERS * len(wls),
+            "breakdown": breakdown,
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_FP16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
+            "traffic": traffic,
+            "kernel": "attn_fwd_kernel",
+            "algorithmic_flops_per_step": total_flops,
+            "algorithmic_bytes_per_step": total_bytes,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    for w in wls:
+        w.free()
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

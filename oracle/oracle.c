@@ -427,6 +427,21 @@ void orc_attention_tiled16(const orc_attn_args* a, uint16_t* out, int64_t o_stri
   free(base);
 }
 
+void orc_attention_tiled16_tiles(const orc_attn_args* a, int32_t seq, int64_t tile_begin,
+                                 int64_t tile_end, int64_t tile_step, uint16_t* out,
+                                 int64_t o_stride) {
+  int64_t t0 = a->cu_seqlens[seq], S = a->cu_seqlens[seq + 1] - t0;
+  int64_t ntiles = (S + 15) / 16;
+  if (tile_end > ntiles) tile_end = ntiles;
+  if (tile_step < 1) tile_step = 1;
+  int64_t count = tile_begin < tile_end ? (tile_end - tile_begin + tile_step - 1) / tile_step : 0;
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int64_t g = 0; g < count * HQ; ++g) {
+    int64_t gx = tile_begin + (g / HQ) * tile_step;
+    tiled16_group(a, t0, S, (int)(g % HQ), gx, out, o_stride);
+  }
+}
+
 void orc_set_threads(int32_t n) {
 #ifdef _OPENMP
   if (n > 0) omp_set_num_threads(n);

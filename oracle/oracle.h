@@ -95,6 +95,12 @@ void orc_attention_exact(const orc_attn_args* a, const int64_t* rows, int64_t nr
  * f16 (V constant in {0.5,1,2}, single key) hold bit-exactly. */
 void orc_attention_tiled16(const orc_attn_args* a, uint16_t* out, int64_t o_stride);
 
+/* The same restatement for the 16-query tiles tile_begin, tile_begin+tile_step, ... < tile_end of
+ * one sequence (all 16 heads): a bounded sample of a long sequence for CPU timing. */
+void orc_attention_tiled16_tiles(const orc_attn_args* a, int32_t seq, int64_t tile_begin,
+                                 int64_t tile_end, int64_t tile_step, uint16_t* out,
+                                 int64_t o_stride);
+
 /* Threads used by the OpenMP loops (0 = runtime default). */
 void orc_set_threads(int32_t n);
 int32_t orc_get_threads(void);

@@ -67,6 +67,8 @@ def lib():
             "orc_ref_tile_skipped": (ctypes.c_int, [i64, i64, i64]),
             "orc_attention_exact": (None, [ctypes.POINTER(_Args), vp, i64, vp]),
             "orc_attention_tiled16": (None, [ctypes.POINTER(_Args), vp, i64]),
+            "orc_attention_tiled16_tiles": (None, [ctypes.POINTER(_Args), i32, i64, i64, i64,
+                                                    vp, i64]),
             "orc_set_threads": (None, [i32]),
             "orc_get_threads": (i32, []),
         }
@@ -207,6 +209,18 @@ def attention_tiled16(q, k, v, cu_seqlens, kind=MASK_PREFIX_LOCAL, prefix=176, w
     T = int(cu[-1])
     out = np.zeros((T, HQ * HD), dtype=np.uint16)
     lib().orc_attention_tiled16(ctypes.byref(a), _ptr(out), HQ * HD)
+    return out
+
+
+def attention_tiled16_tiles(q, k, v, cu_seqlens, seq, tile_begin, tile_end, tile_step,
+                            kind=MASK_PREFIX_LOCAL, prefix=176, window=432, out=None):
+    """Restatement over a strided subset of one sequence's 16-query tiles (CPU timing sample)."""
+    a, cu = _args(q, k, v, cu_seqlens, kind, prefix, window)
+    T = int(cu[-1])
+    if out is None:
+        out = np.zeros((T, HQ * HD), dtype=np.uint16)
+    lib().orc_attention_tiled16_tiles(ctypes.byref(a), seq, tile_begin, tile_end, tile_step,
+                                      _ptr(out), HQ * HD)
     return out
 
 
