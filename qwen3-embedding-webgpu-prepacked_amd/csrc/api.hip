@@ -148,9 +148,15 @@ int validate_desc(qattn_ctx* ctx, const qattn_run_desc* d) {
   int rc = validate_cu(ctx, d->cu_seqlens, d->nseq);
   if (rc) return rc;
   const int64_t T = d->cu_seqlens[d->nseq];
-  const int64_t max_rows = (int64_t)1 << 31;
-  if (T * d->q_row_stride >= max_rows * 64 || T >= max_rows)
-    return fail(ctx, QATTN_EINVAL, "too many tokens (%lld)", (long long)T);
+  if (T >= ((int64_t)1 << 31)) return fail(ctx, QATTN_EINVAL, "too many tokens (%lld)", (long long)T);
+  // The kernel addresses one sequence's rows with 32-bit byte offsets.
+  const int64_t max_stride = std::max(std::max(d->q_row_stride, d->k_row_stride), d->v_row_stride);
+  for (int32_t s = 0; s < d->nseq; ++s) {
+    const int64_t L = d->cu_seqlens[s + 1] - d->cu_seqlens[s];
+    if (L * max_stride * 2 >= ((int64_t)1 << 31))
+      return fail(ctx, QATTN_EINVAL, "sequence %d: %lld tokens x row stride %lld exceeds 2 GiB", s,
+                  (long long)L, (long long)max_stride);
+  }
   return QATTN_OK;
 }
 
@@ -316,15 +322,8 @@ int plan_work(qattn_ctx* ctx, const qattn_run_desc* d, std::vector<WorkItem>* ou
       const int q0 = qb * kBlockQ, q1 = std::min(L, q0 + kBlockQ) - 1;
       const TileRanges tr = key_tiles(q0, q1, L, mask);
       // MFMA tile work of one query head: the wavefronts holding rows [q0, q0+31] and
-      // [q0+32, q0+63] each compute the tiles tile_any() admits for their rows.
-      int cost = 0;
-      for (int half = 0; half < 2; ++half) {
-        const int wq0 = q0 + half * kWaveQ;
-        if (wq0 >= L) continue;
-        const int wq1 = std::min(L - 1, wq0 + kWaveQ - 1);
-        for (int i = 0; i < tr.count(); ++i)
-          if (tile_any(tr.at(i) * kTileK, wq0, wq1, L, mask)) ++cost;
-      }
+      // [q0+32, q0+63] each compute every tile of the work item.
+      const int cost = tr.count() * (q0 + kWaveQ < L ? 2 : 1);
       info.tile_pairs += (int64_t)cost * kWaveQ * kTileK;
       for (int g = 0; g < kKVHeads; ++g)
         items.push_back({WorkItem{start, L, qb, (s << 4) | g}, tr.count() * 256 + cost});

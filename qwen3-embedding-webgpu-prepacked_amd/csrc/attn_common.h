@@ -14,8 +14,8 @@ constexpr int kGroup = kQHeads / kKVHeads;  // ops.ts:196 kv_head = q_head / 2
 
 constexpr int kBlockQ = 64;   // query positions per work item (x 2 heads of one KV group)
 constexpr int kTileK = 64;    // keys per LDS tile
-constexpr int kWaveQ = 32;    // query positions per wavefront (one 32-row MFMA tile)
-constexpr int kWaves = kGroup * kBlockQ / kWaveQ;  // 4
+constexpr int kWaveQ = 32;    // query positions per wavefront (one 32-row MFMA tile, one head)
+constexpr int kWaves = kGroup * kBlockQ / kWaveQ;  // 4: 2 heads x 2 groups of 32 positions
 constexpr int kThreads = kWaves * 64;
 
 struct MaskSpec {
@@ -68,17 +68,6 @@ __host__ __device__ inline TileRanges key_tiles(int qa, int qb, int S, const Mas
   return r;
 }
 
-// Does key tile [kb, kb+kTileK) hold any candidate key for rows [qa, qb]?  Conservative (may
-// answer true for a tile with no retained key; never false for one with a retained key).
-__host__ __device__ inline bool tile_any(int kb, int qa, int qb, int S, const MaskSpec& m) {
-  if (kb > qb) return false;
-  if (m.kind == 0) return true;
-  const int ps = S < m.prefix ? S : m.prefix;
-  const int ws = S < m.window ? S : m.window;
-  const int ke = kb + kTileK - 1;
-  return kb < ps || ke >= qa - ws + 1;
-}
-
 // Is every key of the tile retained for every row in [qa, qb]?  Then no element mask is needed.
 __host__ __device__ inline bool tile_full(int kb, int qa, int qb, int S, const MaskSpec& m) {
   const int ke = kb + kTileK - 1;
@@ -89,28 +78,35 @@ __host__ __device__ inline bool tile_full(int kb, int qa, int qb, int S, const M
   return ke < ps || qb - kb < ws;
 }
 
+// Element rule the kernel applies on tiles that are not tile_full, with ps = min(S, prefix) and
+// ws = min(S, window) precomputed.  For a query row q < S it equals retained(q, key, S, m):
+// key <= q implies key < S, and key + ws > q is key >= q - ws + 1.
+__host__ __device__ inline bool keep_key(int q, int key, int ps, int ws, int kind) {
+  return key <= q && (kind == 0 || key < ps || key >= q - ws + 1);
+}
+
 // Keys the attention kernel keeps for query row q of a sequence of length S, as a bitmask row
 // (word k/32, bit k%32; `row` pre-zeroed, `words` = ceil(S/32)).  Walks the kernel's own
-// iteration: the work item's tile ranges (key_tiles over its 64 rows), the wavefront's tile test
-// (tile_any over its 32 rows) and the element rule (tile_full, else retained).
+// iteration: every wavefront of a work item visits the work item's tile ranges (key_tiles over
+// its 64 rows); a tile that is tile_full for the wavefront's 32 rows keeps all its keys,
+// any other tile keeps the keys keep_key() admits.
 __host__ __device__ inline void kept_keys_row(int q, int S, const MaskSpec& m, uint32_t* row,
                                               int words) {
   const int blk_q0 = (q / kBlockQ) * kBlockQ;
   const int blk_q1 = (S < blk_q0 + kBlockQ ? S : blk_q0 + kBlockQ) - 1;
   const int wq0 = (q / kWaveQ) * kWaveQ;
   const int wq1 = (S - 1 < wq0 + kWaveQ - 1) ? S - 1 : wq0 + kWaveQ - 1;
+  const int ps = S < m.prefix ? S : m.prefix;
+  const int ws = S < m.window ? S : m.window;
   const TileRanges tiles = key_tiles(blk_q0, blk_q1, S, m);
   for (int it = 0; it < tiles.count(); ++it) {
     const int kb = tiles.at(it) * kTileK;
-    if (!tile_any(kb, wq0, wq1, S, m)) continue;
     const bool full = tile_full(kb, wq0, wq1, S, m);
     for (int wd = 0; wd < kTileK / 32; ++wd) {
       uint32_t word = 0;
       for (int b = 0; b < 32; ++b) {
         const int key = kb + 32 * wd + b;
-        // Keys >= S are zero-filled in LDS and dropped by retained(); a full tile has
-        // every key <= its first row < S.
-        if (key < S && (full || retained(q, key, S, m))) word |= 1u << b;
+        if (full || keep_key(q, key, ps, ws, m.kind)) word |= 1u << b;
       }
       const int wi = kb / 32 + wd;
       if (wi < words) row[wi] = word;

@@ -130,6 +130,14 @@ def test_validation_nseq_zero_and_null(qattn):
         qattn.plan_describe(d)
 
 
+def test_validation_rejects_sequences_beyond_32bit_offsets(qattn):
+    d = _desc(qattn, [300000], v_row_stride=4096)
+    with pytest.raises(qattn.QattnError) as e:
+        qattn.plan_describe(d)
+    assert "2 GiB" in str(e.value)
+    qattn.plan_describe(_desc(qattn, [200000]))  # 200000 x 2048 x 2 B < 2 GiB
+
+
 def test_empty_sequences_are_skipped(qattn):
     items, info = qattn.plan_describe(_desc(qattn, [0, 7, 0, 0, 70]))
     assert info.tokens == 77 and info.work_items == 8 * (1 + 2)
