@@ -162,6 +162,14 @@ int qattn_qk_norm_rope(qattn_ctx* ctx, void* x, int64_t row_stride, int64_t col0
  * e>>1 of the SplitMix64(seed) stream (outputs e&~1 and e|1), cos for even e, sin for odd e. */
 int qattn_fill_normal(qattn_ctx* ctx, void* dst, int64_t rows, int64_t row_elems,
                       int64_t row_stride, uint64_t seed, qattn_stream_t stream);
+/* Row r (r < rows) of dst receives row_elems fp16 N(0,1) draws keyed by the token id ids[r]
+ * (device int32 array): draw c comes from the SplitMix64 stream seeded with
+ * seed + (uint32)ids[r] * 0xD1B54A32D192ED03, paired as in qattn_fill_normal.  A stand-in for
+ * the projections that produce Q/K/V from token embeddings (outside this library), so that an
+ * engine driving the attention path sees outputs that depend on its token ids. */
+int qattn_fill_token_rows(qattn_ctx* ctx, void* dst, const int32_t* ids, int64_t rows,
+                          int64_t row_elems, int64_t row_stride, uint64_t seed,
+                          qattn_stream_t stream);
 /* Seeded Q/K/V of one (config, layer): raw N(0,1) fp16 Q [T,16,128], K [T,8,128],
  * V [T,8,128] (seeds 0x51574E33_00000000 | config<<16 | layer<<8 | tensor), then
  * qattn_qk_norm_rope on Q and K (unit gain, eps 1e-6, theta 1e6). */

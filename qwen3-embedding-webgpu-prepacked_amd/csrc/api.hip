@@ -42,6 +42,8 @@ hipError_t launch_debug_mask(int S, MaskSpec mask, uint32_t* bits, int words_per
                              hipStream_t stream);
 hipError_t launch_fill_normal(half_t* dst, int64_t rows, int64_t row_elems, int64_t row_stride,
                               uint64_t seed, hipStream_t stream);
+hipError_t launch_fill_token_rows(half_t* dst, const int32_t* ids, int64_t rows, int64_t row_elems,
+                                  int64_t row_stride, uint64_t seed, hipStream_t stream);
 hipError_t launch_qk_norm_rope(half_t* x, int64_t row_stride, int64_t col0, int heads,
                                const int32_t* cu_dev, int nseq, int64_t T, const float* weight,
                                double eps, const float* rope_cos, const float* rope_sin,
@@ -556,6 +558,18 @@ int qattn_fill_normal(qattn_ctx* ctx, void* dst, int64_t rows, int64_t row_elems
   DeviceGuard g(ctx->device);
   HIP_TRY(ctx, launch_fill_normal(static_cast<half_t*>(dst), rows, row_elems, row_stride, seed,
                                   pick_stream(ctx, stream)));
+  return QATTN_OK;
+}
+
+int qattn_fill_token_rows(qattn_ctx* ctx, void* dst, const int32_t* ids, int64_t rows,
+                          int64_t row_elems, int64_t row_stride, uint64_t seed,
+                          qattn_stream_t stream) {
+  if (!ctx || !dst || (!ids && rows)) return fail(ctx, QATTN_EINVAL, "NULL argument");
+  if (rows < 0 || row_elems < 0 || row_stride < row_elems)
+    return fail(ctx, QATTN_EINVAL, "bad rows/row_elems/row_stride");
+  DeviceGuard g(ctx->device);
+  HIP_TRY(ctx, launch_fill_token_rows(static_cast<half_t*>(dst), ids, rows, row_elems, row_stride,
+                                      seed, pick_stream(ctx, stream)));
   return QATTN_OK;
 }
 

@@ -84,6 +84,37 @@ __global__ void qk_norm_rope_kernel(half_t* x, int64_t row_stride, int64_t col0,
   }
 }
 
+// Row r of dst gets N(0,1) draws keyed by the token id ids[r]: element c is draw c of the
+// stream seeded with seed + ids[r] * 0xD1B54A32D192ED03 (same pairing as fill_normal_kernel).
+__global__ void fill_token_rows_kernel(half_t* dst, const int32_t* ids, int64_t rows,
+                                       int64_t row_elems, int64_t row_stride, uint64_t seed) {
+  const int64_t pairs_per_row = (row_elems + 1) / 2;
+  const int64_t total = rows * pairs_per_row;
+  for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < total;
+       g += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = g / pairs_per_row, j = g % pairs_per_row;
+    const uint64_t s = seed + (uint64_t)(uint32_t)ids[r] * 0xD1B54A32D192ED03ULL;
+    const double u1 = (double)((rand_u64(s, 2 * j) >> 11) + 1) * 0x1.0p-53;
+    const double u2 = (double)(rand_u64(s, 2 * j + 1) >> 11) * 0x1.0p-53;
+    const double rr = sqrt(-2.0 * log(u1));
+    double sn, cs;
+    sincos(6.283185307179586 * u2, &sn, &cs);
+    dst[r * row_stride + 2 * j] = to_half((float)(rr * cs));
+    if (2 * j + 1 < row_elems) dst[r * row_stride + 2 * j + 1] = to_half((float)(rr * sn));
+  }
+}
+
+hipError_t launch_fill_token_rows(half_t* dst, const int32_t* ids, int64_t rows, int64_t row_elems,
+                                  int64_t row_stride, uint64_t seed, hipStream_t stream) {
+  const int64_t total = rows * ((row_elems + 1) / 2);
+  if (total <= 0) return hipSuccess;
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(fill_token_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, dst, ids,
+                     rows, row_elems, row_stride, seed);
+  return hipGetLastError();
+}
+
 hipError_t launch_fill_normal(half_t* dst, int64_t rows, int64_t row_elems, int64_t row_stride,
                               uint64_t seed, hipStream_t stream) {
   const int64_t npairs = (rows * row_elems + 1) / 2;

@@ -1,0 +1,648 @@
+// qattn_napi.cc -- Node N-API binding of libqattn.so (C ABI: include/qattn.h).
+//
+// This is the seam the reference engine reaches through WebGPU (src/webgpu/device.ts,
+// src/webgpu/ops.ts:318-345): device context, device buffers, the attention operator
+// (createRun / encode / destroy), the mask check and the producer kernels.  Device resources are
+// N-API externals; every failure of the C ABI becomes a thrown JavaScript Error carrying
+// qattn_last_error() (the reference throws synchronously on contract violations, model.ts:114).
+// synchronizeAsync() waits for the context stream on a worker thread and returns a Promise, so
+// the engine's run() stays asynchronous like the reference's mapAsync readback (model.ts:135).
+#include <node_api.h>
+
+#include <cstdint>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../../include/qattn.h"
+
+namespace {
+
+#define NAPI_OK(env, call)                                                       \
+  do {                                                                           \
+    if ((call) != napi_ok) {                                                     \
+      const napi_extended_error_info* info_ = nullptr;                           \
+      napi_get_last_error_info((env), &info_);                                   \
+      napi_throw_error((env), nullptr,                                           \
+                       info_ && info_->error_message ? info_->error_message      \
+                                                     : "N-API call failed");    \
+      return nullptr;                                                            \
+    }                                                                            \
+  } while (0)
+
+struct Ctx {
+  qattn_ctx* ctx = nullptr;
+};
+struct Buf {
+  Ctx* owner = nullptr;
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+struct Run {
+  qattn_run* run = nullptr;
+};
+
+napi_value throw_qattn(napi_env env, int rc, const qattn_ctx* ctx) {
+  std::string msg = "qattn error " + std::to_string(rc) + ": " + qattn_last_error(ctx);
+  napi_throw_error(env, std::to_string(rc).c_str(), msg.c_str());
+  return nullptr;
+}
+
+napi_value undefined(napi_env env) {
+  napi_value u;
+  napi_get_undefined(env, &u);
+  return u;
+}
+
+template <typename T>
+T* get_external(napi_env env, napi_value v, const char* what) {
+  void* data = nullptr;
+  if (napi_get_value_external(env, v, &data) != napi_ok || !data) {
+    napi_throw_type_error(env, nullptr, (std::string("expected ") + what).c_str());
+    return nullptr;
+  }
+  return static_cast<T*>(data);
+}
+
+bool get_i64(napi_env env, napi_value v, int64_t* out) {
+  napi_valuetype t;
+  if (napi_typeof(env, v, &t) != napi_ok || t != napi_number) return false;
+  return napi_get_value_int64(env, v, out) == napi_ok;
+}
+
+bool prop(napi_env env, napi_value obj, const char* name, napi_value* out) {
+  bool has = false;
+  if (napi_has_named_property(env, obj, name, &has) != napi_ok || !has) return false;
+  if (napi_get_named_property(env, obj, name, out) != napi_ok) return false;
+  napi_valuetype t;
+  napi_typeof(env, *out, &t);
+  return t != napi_undefined && t != napi_null;
+}
+
+// Typed array (or Buffer) view: data pointer and byte length.
+bool typed_bytes(napi_env env, napi_value v, void** data, size_t* bytes) {
+  bool is_ta = false;
+  napi_is_typedarray(env, v, &is_ta);
+  if (is_ta) {
+    napi_typedarray_type type;
+    size_t length = 0, offset = 0;
+    napi_value ab;
+    if (napi_get_typedarray_info(env, v, &type, &length, data, &ab, &offset) != napi_ok) return false;
+    size_t elem = 1;
+    switch (type) {
+      case napi_int16_array: case napi_uint16_array: elem = 2; break;
+      case napi_int32_array: case napi_uint32_array: case napi_float32_array: elem = 4; break;
+      case napi_float64_array: case napi_bigint64_array: case napi_biguint64_array: elem = 8; break;
+      default: elem = 1;
+    }
+    *bytes = length * elem;
+    return true;
+  }
+  bool is_buf = false;
+  napi_is_buffer(env, v, &is_buf);
+  if (is_buf) return napi_get_buffer_info(env, v, data, bytes) == napi_ok;
+  return false;
+}
+
+void finalize_ctx(napi_env, void* data, void*) {
+  auto* c = static_cast<Ctx*>(data);
+  if (c->ctx) qattn_destroy(c->ctx);
+  delete c;
+}
+void finalize_buf(napi_env, void* data, void*) {
+  // Device memory is released by free(); a collected handle that was never freed is released
+  // here if its context still exists.
+  auto* b = static_cast<Buf*>(data);
+  if (b->ptr && b->owner && b->owner->ctx) qattn_buffer_free(b->owner->ctx, b->ptr);
+  delete b;
+}
+void finalize_run(napi_env, void* data, void*) {
+  auto* r = static_cast<Run*>(data);
+  if (r->run) qattn_run_destroy(r->run);
+  delete r;
+}
+
+napi_value args_of(napi_env env, napi_callback_info info, size_t want, napi_value* argv) {
+  size_t argc = want;
+  NAPI_OK(env, napi_get_cb_info(env, info, &argc, argv, nullptr, nullptr));
+  if (argc < want) {
+    napi_throw_type_error(env, nullptr, "missing arguments");
+    return nullptr;
+  }
+  return undefined(env);
+}
+
+// createContext(device) -> external
+napi_value CreateContext(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!args_of(env, info, 1, argv)) return nullptr;
+  int64_t device = 0;
+  if (!get_i64(env, argv[0], &device)) {
+    napi_throw_type_error(env, nullptr, "device must be a number");
+    return nullptr;
+  }
+  qattn_ctx* ctx = nullptr;
+  int rc = qattn_create((int)device, &ctx);
+  if (rc) return throw_qattn(env, rc, nullptr);
+  auto* c = new Ctx{ctx};
+  napi_value out;
+  NAPI_OK(env, napi_create_external(env, c, finalize_ctx, nullptr, &out));
+  return out;
+}
+
+napi_value DestroyContext(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!args_of(env, info, 1, argv)) return nullptr;
+  Ctx* c = get_external<Ctx>(env, argv[0], "context");
+  if (!c) return nullptr;
+  if (c->ctx) qattn_destroy(c->ctx);
+  c->ctx = nullptr;
+  return undefined(env);
+}
+
+Ctx* live_ctx(napi_env env, napi_value v) {
+  Ctx* c = get_external<Ctx>(env, v, "context");
+  if (c && !c->ctx) {
+    napi_throw_error(env, nullptr, "context was destroyed");
+    return nullptr;
+  }
+  return c;
+}
+
+// deviceName(ctx) -> {name, computeUnits}
+napi_value DeviceName(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!args_of(env, info, 1, argv)) return nullptr;
+  Ctx* c = live_ctx(env, argv[0]);
+  if (!c) return nullptr;
+  char name[256];
+  int cus = 0;
+  int rc = qattn_device_name(c->ctx, name, sizeof(name), &cus);
+  if (rc) return throw_qattn(env, rc, c->ctx);
+  napi_value out, n, u;
+  NAPI_OK(env, napi_create_object(env, &out));
+  NAPI_OK(env, napi_create_string_utf8(env, name, NAPI_AUTO_LENGTH, &n));
+  NAPI_OK(env, napi_create_int32(env, cus, &u));
+  NAPI_OK(env, napi_set_named_property(env, out, "name", n));
+  NAPI_OK(env, napi_set_named_property(env, out, "computeUnits", u));
+  return out;
+}
+
+// alloc(ctx, bytes) -> external device buffer
+napi_value Alloc(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!args_of(env, info, 2, argv)) return nullptr;
+  Ctx* c = live_ctx(env, argv[0]);
+  int64_t bytes = 0;
+  if (!c) return nullptr;
+  if (!get_i64(env, argv[1], &bytes) || bytes < 0) {
+    napi_throw_range_error(env, nullptr, "bytes must be a non-negative number");
+    return nullptr;
+  }
+  void* ptr = nullptr;
+  int rc = qattn_buffer_alloc(c->ctx, (size_t)bytes, &ptr);
+  if (rc) return throw_qattn(env, rc, c->ctx);
+  auto* b = new Buf{c, ptr, (size_t)bytes};
+  napi_value out;
+  NAPI_OK(env, napi_create_external(env, b, finalize_buf, nullptr, &out));
+  return out;
+}
+
+napi_value Free(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!args_of(env, info, 1, argv)) return nullptr;
+  Buf* b = get_external<Buf>(env, argv[0], "device buffer");
+  if (!b) return nullptr;
+  if (b->ptr && b->owner->ctx) {
+    int rc = qattn_buffer_free(b->owner->ctx, b->ptr);
+    if (rc) return throw_qattn(env, rc, b->owner->ctx);
+  }
+  b->ptr = nullptr;
+  return undefined(env);
+}
+
+Buf* live_buf(napi_env env, napi_value v) {
+  Buf* b = get_external<Buf>(env, v, "device buffer");
+  if (b && (!b->ptr || !b->owner->ctx)) {
+    napi_throw_error(env, nullptr, "device buffer was freed");
+    return nullptr;
+  }
+  return b;
+}
+
+// write(buf, typedArray, byteOffset=0) / read(buf, typedArray, byteOffset=0)
+napi_value Copy(napi_env env, napi_callback_info info, bool to_device) {
+  napi_value argv[3];
+  size_t argc = 3;
+  NAPI_OK(env, napi_get_cb_info(env, info, &argc, argv, nullptr, nullptr));
+  if (argc < 2) {
+    napi_throw_type_error(env, nullptr, "missing arguments");
+    return nullptr;
+  }
+  Buf* b = live_buf(env, argv[0]);
+  if (!b) return nullptr;
+  void* host = nullptr;
+  size_t bytes = 0;
+  if (!typed_bytes(env, argv[1], &host, &bytes)) {
+    napi_throw_type_error(env, nullptr, "expected a TypedArray or Buffer");
+    return nullptr;
+  }
+  int64_t offset = 0;
+  if (argc > 2 && !get_i64(env, argv[2], &offset)) offset = 0;
+  if (offset < 0 || (size_t)offset + bytes > b->bytes) {
+    napi_throw_range_error(env, nullptr, "copy exceeds the device buffer");
+    return nullptr;
+  }
+  int rc = to_device ? qattn_buffer_write(b->owner->ctx, b->ptr, (size_t)offset, host, bytes)
+                     : qattn_buffer_read(b->owner->ctx, b->ptr, (size_t)offset, host, bytes);
+  if (rc) return throw_qattn(env, rc, b->owner->ctx);
+  return undefined(env);
+}
+napi_value Write(napi_env env, napi_callback_info info) { return Copy(env, info, true); }
+napi_value Read(napi_env env, napi_callback_info info) { return Copy(env, info, false); }
+
+bool get_i32_array(napi_env env, napi_value v, std::vector<int32_t>* out) {
+  void* data = nullptr;
+  size_t bytes = 0;
+  bool is_ta = false;
+  napi_is_typedarray(env, v, &is_ta);
+  if (is_ta) {
+    napi_typedarray_type type;
+    size_t length = 0, offset = 0;
+    napi_value ab;
+    if (napi_get_typedarray_info(env, v, &type, &length, &data, &ab, &offset) != napi_ok) return false;
+    if (type == napi_int32_array || type == napi_uint32_array) {
+      out->assign(static_cast<int32_t*>(data), static_cast<int32_t*>(data) + length);
+      return true;
+    }
+    return false;
+  }
+  bool is_arr = false;
+  napi_is_array(env, v, &is_arr);
+  if (!is_arr) return false;
+  uint32_t n = 0;
+  napi_get_array_length(env, v, &n);
+  out->resize(n);
+  for (uint32_t i = 0; i < n; ++i) {
+    napi_value e;
+    int64_t x = 0;
+    napi_get_element(env, v, i, &e);
+    if (!get_i64(env, e, &x)) return false;
+    (*out)[i] = (int32_t)x;
+  }
+  (void)bytes;
+  return true;
+}
+
+// Fills a qattn_run_desc from a JS descriptor object.  Device tensors are buffer externals with
+// optional byte offsets (qOffsetBytes, ...), strides in elements.
+bool read_desc(napi_env env, napi_value d, qattn_run_desc* desc, std::vector<int32_t>* cu,
+               bool need_device) {
+  std::memset(desc, 0, sizeof(*desc));
+  napi_value v;
+  auto ptr_of = [&](const char* name, const char* off_name, const void** out, bool required) {
+    if (!prop(env, d, name, &v)) {
+      if (required) napi_throw_type_error(env, nullptr, (std::string("missing ") + name).c_str());
+      return !required;
+    }
+    if (!need_device) {
+      // host-only planning: any non-null stand-in address is fine
+      *out = reinterpret_cast<const void*>(uintptr_t(0x100000));
+      return true;
+    }
+    Buf* b = live_buf(env, v);
+    if (!b) return false;
+    int64_t off = 0;
+    napi_value ov;
+    if (prop(env, d, off_name, &ov)) get_i64(env, ov, &off);
+    *out = static_cast<const char*>(b->ptr) + off;
+    return true;
+  };
+  const void *q, *k, *vv, *o, *ol = nullptr;
+  if (!ptr_of("q", "qOffsetBytes", &q, true) || !ptr_of("k", "kOffsetBytes", &k, true) ||
+      !ptr_of("v", "vOffsetBytes", &vv, true) || !ptr_of("o", "oOffsetBytes", &o, true) ||
+      !ptr_of("oLast", "oLastOffsetBytes", &ol, false))
+    return false;
+  desc->q = q;
+  desc->k = k;
+  desc->v = vv;
+  desc->o = const_cast<void*>(o);
+  desc->o_last = const_cast<void*>(ol);
+  auto num = [&](const char* name, int64_t dflt) {
+    int64_t x = dflt;
+    if (prop(env, d, name, &v)) get_i64(env, v, &x);
+    return x;
+  };
+  desc->q_row_stride = num("qRowStride", 2048);
+  desc->k_row_stride = num("kRowStride", 1024);
+  desc->v_row_stride = num("vRowStride", 1024);
+  desc->o_row_stride = num("oRowStride", 2048);
+  desc->v_offset = num("vOffset", 0);
+  desc->mask = (int32_t)num("mask", QATTN_MASK_PREFIX_LOCAL);
+  desc->prefix = (int32_t)num("prefix", 176);
+  desc->window = (int32_t)num("window", 432);
+  if (!prop(env, d, "cuSeqlens", &v) || !get_i32_array(env, v, cu) || cu->size() < 2) {
+    napi_throw_type_error(env, nullptr, "cuSeqlens must be an Int32Array of nseq+1 offsets");
+    return false;
+  }
+  desc->cu_seqlens = cu->data();
+  desc->nseq = (int32_t)cu->size() - 1;
+  return true;
+}
+
+napi_value info_object(napi_env env, const qattn_run_info& i) {
+  napi_value out, x;
+  napi_create_object(env, &out);
+  auto set = [&](const char* n, double val) {
+    napi_create_double(env, val, &x);
+    napi_set_named_property(env, out, n, x);
+  };
+  set("tokens", (double)i.tokens);
+  set("pairs", (double)i.pairs);
+  set("flops", (double)i.flops);
+  set("bytes", (double)i.bytes);
+  set("workItems", i.work_items);
+  set("blockQueries", i.block_queries);
+  set("tilePairs", (double)i.tile_pairs);
+  return out;
+}
+
+// createRun(ctx, desc) -> external run  (reference: CausalAttentionKernel.createRun)
+napi_value CreateRun(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!args_of(env, info, 2, argv)) return nullptr;
+  Ctx* c = live_ctx(env, argv[0]);
+  if (!c) return nullptr;
+  qattn_run_desc desc;
+  std::vector<int32_t> cu;
+  if (!read_desc(env, argv[1], &desc, &cu, true)) return nullptr;
+  qattn_run* run = nullptr;
+  int rc = qattn_run_create(c->ctx, &desc, &run);
+  if (rc) return throw_qattn(env, rc, c->ctx);
+  auto* r = new Run{run};
+  napi_value out;
+  NAPI_OK(env, napi_create_external(env, r, finalize_run, nullptr, &out));
+  return out;
+}
+
+Run* live_run(napi_env env, napi_value v) {
+  Run* r = get_external<Run>(env, v, "attention run");
+  if (r && !r->run) {
+    napi_throw_error(env, nullptr, "attention run was destroyed");
+    return nullptr;
+  }
+  return r;
+}
+
+// encode(run)  (reference: CausalAttentionKernel.encode(pass, run))
+napi_value Encode(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!args_of(env, info, 1, argv)) return nullptr;
+  Run* r = live_run(env, argv[0]);
+  if (!r) return nullptr;
+  int rc = qattn_run_encode(r->run, nullptr);
+  if (rc) return throw_qattn(env, rc, nullptr);
+  return undefined(env);
+}
+
+napi_value DestroyRun(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!args_of(env, info, 1, argv)) return nullptr;
+  Run* r = get_external<Run>(env, argv[0], "attention run");
+  if (!r) return nullptr;
+  if (r->run) qattn_run_destroy(r->run);
+  r->run = nullptr;
+  return undefined(env);
+}
+
+napi_value RunInfo(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!args_of(env, info, 1, argv)) return nullptr;
+  Run* r = live_run(env, argv[0]);
+  if (!r) return nullptr;
+  qattn_run_info i{};
+  int rc = qattn_run_get_info(r->run, &i);
+  if (rc) return throw_qattn(env, rc, nullptr);
+  return info_object(env, i);
+}
+
+// planDescribe(desc) -> {items: Int32Array (n*4), info}; host only, no device needed.
+napi_value PlanDescribe(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!args_of(env, info, 1, argv)) return nullptr;
+  qattn_run_desc desc;
+  std::vector<int32_t> cu;
+  if (!read_desc(env, argv[0], &desc, &cu, false)) return nullptr;
+  int32_t n = 0;
+  qattn_run_info i{};
+  int rc = qattn_plan_describe(&desc, nullptr, 0, &n, &i);
+  if (rc) return throw_qattn(env, rc, nullptr);
+  napi_value ab, arr, out;
+  void* data = nullptr;
+  NAPI_OK(env, napi_create_arraybuffer(env, (size_t)n * 16, &data, &ab));
+  if (n) {
+    rc = qattn_plan_describe(&desc, static_cast<int32_t*>(data), n, &n, nullptr);
+    if (rc) return throw_qattn(env, rc, nullptr);
+  }
+  NAPI_OK(env, napi_create_typedarray(env, napi_int32_array, (size_t)n * 4, ab, 0, &arr));
+  NAPI_OK(env, napi_create_object(env, &out));
+  NAPI_OK(env, napi_set_named_property(env, out, "items", arr));
+  NAPI_OK(env, napi_set_named_property(env, out, "info", info_object(env, i)));
+  return out;
+}
+
+// planMask(L, mask, prefix, window) -> Uint32Array (host evaluation of the kernel iteration)
+// debugMask(ctx, L, mask, prefix, window) -> Uint32Array (device)
+napi_value MaskCommon(napi_env env, napi_callback_info info, bool device) {
+  napi_value argv[5];
+  const size_t want = device ? 5 : 4;
+  if (!args_of(env, info, want, argv)) return nullptr;
+  int off = device ? 1 : 0;
+  int64_t L = 0, mask = 1, prefix = 176, window = 432;
+  if (!get_i64(env, argv[off], &L) || !get_i64(env, argv[off + 1], &mask) ||
+      !get_i64(env, argv[off + 2], &prefix) || !get_i64(env, argv[off + 3], &window) || L < 0) {
+    napi_throw_type_error(env, nullptr, "expected (L, mask, prefix, window) numbers");
+    return nullptr;
+  }
+  const size_t words = (size_t)((L + 31) / 32) * (size_t)L;
+  napi_value ab, arr;
+  void* data = nullptr;
+  NAPI_OK(env, napi_create_arraybuffer(env, words * 4, &data, &ab));
+  int rc;
+  if (device) {
+    Ctx* c = live_ctx(env, argv[0]);
+    if (!c) return nullptr;
+    rc = qattn_debug_mask(c->ctx, (int32_t)L, (int32_t)mask, (int32_t)prefix, (int32_t)window,
+                          static_cast<uint32_t*>(data));
+    if (rc) return throw_qattn(env, rc, c->ctx);
+  } else {
+    rc = qattn_plan_mask((int32_t)L, (int32_t)mask, (int32_t)prefix, (int32_t)window,
+                         static_cast<uint32_t*>(data));
+    if (rc) return throw_qattn(env, rc, nullptr);
+  }
+  NAPI_OK(env, napi_create_typedarray(env, napi_uint32_array, words, ab, 0, &arr));
+  return arr;
+}
+napi_value PlanMask(napi_env env, napi_callback_info info) { return MaskCommon(env, info, false); }
+napi_value DebugMask(napi_env env, napi_callback_info info) { return MaskCommon(env, info, true); }
+
+// genQkv(ctx, config, layer, cuSeqlens, q, k, v)  (compact layouts)
+napi_value GenQkv(napi_env env, napi_callback_info info) {
+  napi_value argv[7];
+  if (!args_of(env, info, 7, argv)) return nullptr;
+  Ctx* c = live_ctx(env, argv[0]);
+  if (!c) return nullptr;
+  int64_t config = 0, layer = 0;
+  std::vector<int32_t> cu;
+  if (!get_i64(env, argv[1], &config) || !get_i64(env, argv[2], &layer) ||
+      !get_i32_array(env, argv[3], &cu) || cu.size() < 2) {
+    napi_throw_type_error(env, nullptr, "expected (ctx, config, layer, cuSeqlens, q, k, v)");
+    return nullptr;
+  }
+  Buf *q = live_buf(env, argv[4]), *k = q ? live_buf(env, argv[5]) : nullptr,
+      *v = k ? live_buf(env, argv[6]) : nullptr;
+  if (!v) return nullptr;
+  int rc = qattn_gen_qkv(c->ctx, (uint32_t)config, (uint32_t)layer, cu.data(), (int32_t)cu.size() - 1,
+                         q->ptr, 2048, k->ptr, 1024, v->ptr, 1024, nullptr);
+  if (rc) return throw_qattn(env, rc, c->ctx);
+  return undefined(env);
+}
+
+// fillTokenRows(ctx, dst, ids(device buffer), rows, rowElems, rowStride, seedHi, seedLo)
+napi_value FillTokenRows(napi_env env, napi_callback_info info) {
+  napi_value argv[8];
+  if (!args_of(env, info, 8, argv)) return nullptr;
+  Ctx* c = live_ctx(env, argv[0]);
+  if (!c) return nullptr;
+  Buf *dst = live_buf(env, argv[1]), *ids = dst ? live_buf(env, argv[2]) : nullptr;
+  if (!ids) return nullptr;
+  int64_t rows, elems, stride, hi, lo;
+  if (!get_i64(env, argv[3], &rows) || !get_i64(env, argv[4], &elems) ||
+      !get_i64(env, argv[5], &stride) || !get_i64(env, argv[6], &hi) || !get_i64(env, argv[7], &lo)) {
+    napi_throw_type_error(env, nullptr, "expected numbers");
+    return nullptr;
+  }
+  if ((size_t)rows * 4 > ids->bytes || (size_t)(rows * stride) * 2 > dst->bytes) {
+    napi_throw_range_error(env, nullptr, "rows exceed the buffers");
+    return nullptr;
+  }
+  const uint64_t seed = ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+  int rc = qattn_fill_token_rows(c->ctx, dst->ptr, static_cast<const int32_t*>(ids->ptr), rows,
+                                 elems, stride, seed, nullptr);
+  if (rc) return throw_qattn(env, rc, c->ctx);
+  return undefined(env);
+}
+
+// qkNormRope(ctx, x, rowStride, col0, heads, cuSeqlens, eps, theta)
+napi_value QkNormRope(napi_env env, napi_callback_info info) {
+  napi_value argv[8];
+  if (!args_of(env, info, 8, argv)) return nullptr;
+  Ctx* c = live_ctx(env, argv[0]);
+  if (!c) return nullptr;
+  Buf* x = live_buf(env, argv[1]);
+  if (!x) return nullptr;
+  int64_t stride, col0, heads;
+  double eps = 1e-6, theta = 1e6;
+  std::vector<int32_t> cu;
+  if (!get_i64(env, argv[2], &stride) || !get_i64(env, argv[3], &col0) ||
+      !get_i64(env, argv[4], &heads) || !get_i32_array(env, argv[5], &cu) || cu.size() < 2 ||
+      napi_get_value_double(env, argv[6], &eps) != napi_ok ||
+      napi_get_value_double(env, argv[7], &theta) != napi_ok) {
+    napi_throw_type_error(env, nullptr, "expected (ctx, x, rowStride, col0, heads, cuSeqlens, eps, theta)");
+    return nullptr;
+  }
+  if ((size_t)cu.back() * (size_t)stride * 2 > x->bytes) {
+    napi_throw_range_error(env, nullptr, "rows exceed the buffer");
+    return nullptr;
+  }
+  int rc = qattn_qk_norm_rope(c->ctx, x->ptr, stride, col0, (int32_t)heads, cu.data(),
+                              (int32_t)cu.size() - 1, nullptr, eps, theta, nullptr);
+  if (rc) return throw_qattn(env, rc, c->ctx);
+  return undefined(env);
+}
+
+napi_value Synchronize(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!args_of(env, info, 1, argv)) return nullptr;
+  Ctx* c = live_ctx(env, argv[0]);
+  if (!c) return nullptr;
+  int rc = qattn_synchronize(c->ctx);
+  if (rc) return throw_qattn(env, rc, c->ctx);
+  return undefined(env);
+}
+
+// synchronizeAsync(ctx) -> Promise<void>: waits for the context stream off the JS thread.
+struct SyncWork {
+  napi_async_work work = nullptr;
+  napi_deferred deferred = nullptr;
+  qattn_ctx* ctx = nullptr;
+  int rc = 0;
+  std::string msg;
+};
+void sync_execute(napi_env, void* data) {
+  auto* w = static_cast<SyncWork*>(data);
+  w->rc = qattn_synchronize(w->ctx);
+  if (w->rc) w->msg = qattn_last_error(w->ctx);
+}
+void sync_complete(napi_env env, napi_status, void* data) {
+  auto* w = static_cast<SyncWork*>(data);
+  if (w->rc == 0) {
+    napi_resolve_deferred(env, w->deferred, undefined(env));
+  } else {
+    napi_value m, e;
+    std::string s = "qattn error " + std::to_string(w->rc) + ": " + w->msg;
+    napi_create_string_utf8(env, s.c_str(), NAPI_AUTO_LENGTH, &m);
+    napi_create_error(env, nullptr, m, &e);
+    napi_reject_deferred(env, w->deferred, e);
+  }
+  napi_delete_async_work(env, w->work);
+  delete w;
+}
+napi_value SynchronizeAsync(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!args_of(env, info, 1, argv)) return nullptr;
+  Ctx* c = live_ctx(env, argv[0]);
+  if (!c) return nullptr;
+  auto* w = new SyncWork();
+  w->ctx = c->ctx;
+  napi_value promise, name;
+  NAPI_OK(env, napi_create_promise(env, &w->deferred, &promise));
+  NAPI_OK(env, napi_create_string_utf8(env, "qattn.synchronize", NAPI_AUTO_LENGTH, &name));
+  NAPI_OK(env, napi_create_async_work(env, nullptr, name, sync_execute, sync_complete, w, &w->work));
+  NAPI_OK(env, napi_queue_async_work(env, w->work));
+  return promise;
+}
+
+napi_value AbiVersion(napi_env env, napi_callback_info) {
+  napi_value v;
+  napi_create_int32(env, qattn_abi_version(), &v);
+  return v;
+}
+
+napi_value Init(napi_env env, napi_value exports) {
+  struct Fn {
+    const char* name;
+    napi_callback cb;
+  } fns[] = {
+      {"abiVersion", AbiVersion},     {"createContext", CreateContext},
+      {"destroyContext", DestroyContext}, {"deviceName", DeviceName},
+      {"alloc", Alloc},               {"free", Free},
+      {"write", Write},               {"read", Read},
+      {"createRun", CreateRun},       {"encode", Encode},
+      {"destroyRun", DestroyRun},     {"runInfo", RunInfo},
+      {"planDescribe", PlanDescribe}, {"planMask", PlanMask},
+      {"debugMask", DebugMask},       {"genQkv", GenQkv},
+      {"fillTokenRows", FillTokenRows}, {"qkNormRope", QkNormRope},
+      {"synchronize", Synchronize},   {"synchronizeAsync", SynchronizeAsync},
+  };
+  for (const Fn& f : fns) {
+    napi_value fn;
+    NAPI_OK(env, napi_create_function(env, f.name, NAPI_AUTO_LENGTH, f.cb, nullptr, &fn));
+    NAPI_OK(env, napi_set_named_property(env, exports, f.name, fn));
+  }
+  return exports;
+}
+
+}  // namespace
+
+NAPI_MODULE(qattn_napi, Init)

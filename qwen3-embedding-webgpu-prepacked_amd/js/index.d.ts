@@ -1,0 +1,79 @@
+// Type declarations of the Node attention-path package (js/index.js).  The engine and plugin
+// interfaces match src/webgpu/embedding-engine.ts:1-13 of the reference.
+
+export interface TokenizerResult {
+  input_ids: { tolist(): number[][] };
+}
+export type TokenizerLike = (text: string) => TokenizerResult;
+
+export interface EmbeddingPlan {
+  run(ids: Uint32Array, lengths: Uint32Array): Promise<Float32Array[]>;
+}
+export interface EmbeddingRuntime {
+  /** 'varlen': the engine packs requests back to back (ids.length === sum(lengths)). */
+  packing?: 'padded' | 'varlen';
+  createPlan(batch: number, sequence: number): EmbeddingPlan;
+}
+
+export class Qwen3EmbeddingEngine {
+  constructor(runtime: EmbeddingRuntime, tokenizer: TokenizerLike, maxBatchSize?: number,
+              batchWindowMs?: number, eosToken?: number);
+  readonly maxBatchSize: number;
+  readonly batchWindowMs: number;
+  readonly eosToken: number;
+  embed(text: string): Promise<Float32Array>;
+}
+
+export function packPadded(tokenLists: number[][], eosToken: number): { ids: Uint32Array; lengths: Uint32Array; sequence: number };
+export function packVarlen(tokenLists: number[][]): { ids: Uint32Array; lengths: Uint32Array; sequence: number };
+export function cuSeqlensOf(lengths: ArrayLike<number>): Int32Array;
+
+export type MaskName = 'causal' | 'prefix-local';
+
+export class DeviceBuffer {
+  readonly bytes: number;
+  write(data: ArrayBufferView, byteOffset?: number): void;
+  read<T extends ArrayBufferView>(data: T, byteOffset?: number): T;
+  destroy(): void;
+}
+
+export class DeviceContext {
+  constructor(device?: number);
+  info(): { name: string; computeUnits: number };
+  alloc(bytes: number): DeviceBuffer;
+  synchronize(): void;
+  synchronizeAsync(): Promise<void>;
+  destroy(): void;
+}
+
+export interface RunInfo {
+  tokens: number; pairs: number; flops: number; bytes: number;
+  workItems: number; blockQueries: number; tilePairs: number;
+}
+export interface AttentionRun { handle: unknown; info: RunInfo; cuSeqlens: Int32Array }
+export interface VarlenOptions {
+  queryStride?: number; keyStride?: number; valueStride?: number; outputStride?: number;
+  valueOffset?: number; mask?: MaskName; prefix?: number; window?: number; lastRows?: DeviceBuffer;
+}
+
+export class CausalAttentionKernel {
+  constructor(context: DeviceContext);
+  createRun(q: DeviceBuffer, k: DeviceBuffer, v: DeviceBuffer, output: DeviceBuffer, batch: number,
+            sequence: number, qHeads?: number, kvHeads?: number, valueStride?: number,
+            valueOffset?: number, options?: VarlenOptions): AttentionRun;
+  createVarlenRun(q: DeviceBuffer, k: DeviceBuffer, v: DeviceBuffer, output: DeviceBuffer,
+                  cuSeqlens: ArrayLike<number>, options?: VarlenOptions): AttentionRun;
+  encode(run: AttentionRun): void;
+  destroyRun(run: AttentionRun): void;
+}
+
+export interface HipRuntimeOptions {
+  device?: number; context?: DeviceContext; layers?: number; mask?: MaskName;
+  prefix?: number; window?: number; seed?: number;
+}
+export class HipAttentionRuntime implements EmbeddingRuntime {
+  constructor(options?: HipRuntimeOptions);
+  readonly packing: 'varlen';
+  createPlan(batch: number, sequence: number): EmbeddingPlan;
+  destroy(): void;
+}

@@ -1,0 +1,92 @@
+'use strict';
+// Attention operator over libqattn.so, mirroring the reference's CausalAttentionKernel
+// (src/webgpu/ops.ts:318-345):
+//   createRun(q, k, v, output, batch, sequence, qHeads = 16, kvHeads = 8, valueStride = 1024,
+//             valueOffset = 0) -> AttentionRun      (padded [batch, sequence] layout, ops.ts:327)
+//   encode(run)                                     (ops.ts:344; the stream is the context's)
+//   destroyRun(run)                                 (the run's owned buffers, model.ts:108-111)
+// plus createVarlenRun(q, k, v, output, cuSeqlens, options) for packed sequences.
+// Buffers are device buffers from DeviceContext.alloc().  The mask is the reference's
+// always-on 176-token prefix + 432-token local window (ops.ts:206) unless options say otherwise.
+
+const { loadAddon } = require('./addon');
+
+const MASK = { causal: 0, 'prefix-local': 1 };
+
+function maskCode(name) {
+  if (!(name in MASK)) throw new Error(`unknown mask ${name}; expected 'causal' or 'prefix-local'`);
+  return MASK[name];
+}
+
+class DeviceBuffer {
+  constructor(context, bytes) {
+    this.context = context;
+    this.bytes = bytes;
+    this.handle = context.addon.alloc(context.handle, bytes);
+  }
+  write(typedArray, byteOffset = 0) { this.context.addon.write(this.handle, typedArray, byteOffset); }
+  read(typedArray, byteOffset = 0) { this.context.addon.read(this.handle, typedArray, byteOffset); return typedArray; }
+  destroy() {
+    if (this.handle) this.context.addon.free(this.handle);
+    this.handle = null;
+  }
+}
+
+// One device (reference: requestWebGPUDevice, src/webgpu/device.ts:6-24).
+class DeviceContext {
+  constructor(device = 0) {
+    this.addon = loadAddon();
+    this.handle = this.addon.createContext(device);
+  }
+  info() { return this.addon.deviceName(this.handle); }
+  alloc(bytes) { return new DeviceBuffer(this, bytes); }
+  synchronize() { this.addon.synchronize(this.handle); }
+  synchronizeAsync() { return this.addon.synchronizeAsync(this.handle); }
+  destroy() {
+    if (this.handle) this.addon.destroyContext(this.handle);
+    this.handle = null;
+  }
+}
+
+class CausalAttentionKernel {
+  constructor(context) {
+    this.context = context;
+  }
+
+  // Padded layout exactly as the reference plans it: batch sequences of `sequence` rows each.
+  createRun(q, k, v, output, batch, sequence, qHeads = 16, kvHeads = 8, valueStride = 1024, valueOffset = 0, options = {}) {
+    if (qHeads !== 16 || kvHeads !== 8) throw new Error('only 16 query heads over 8 KV heads (Qwen3-Embedding-0.6B) are supported');
+    const cuSeqlens = new Int32Array(batch + 1);
+    for (let b = 0; b < batch; b += 1) cuSeqlens[b + 1] = cuSeqlens[b] + sequence;
+    return this.createVarlenRun(q, k, v, output, cuSeqlens, Object.assign({ valueStride, valueOffset }, options));
+  }
+
+  // Packed varlen layout: sequence i is rows cuSeqlens[i]..cuSeqlens[i+1]-1.
+  createVarlenRun(q, k, v, output, cuSeqlens, options = {}) {
+    const desc = {
+      q: q.handle, k: k.handle, v: v.handle, o: output.handle,
+      qRowStride: options.queryStride || 2048,
+      kRowStride: options.keyStride || 1024,
+      vRowStride: options.valueStride || 1024,
+      oRowStride: options.outputStride || 2048,
+      vOffset: options.valueOffset || 0,
+      cuSeqlens: Int32Array.from(cuSeqlens),
+      mask: maskCode(options.mask || 'prefix-local'),
+      prefix: options.prefix === undefined ? 176 : options.prefix,
+      window: options.window === undefined ? 432 : options.window,
+    };
+    if (options.lastRows) desc.oLast = options.lastRows.handle;
+    const addon = this.context.addon;
+    const handle = addon.createRun(this.context.handle, desc);
+    return { handle, info: addon.runInfo(handle), cuSeqlens: desc.cuSeqlens };
+  }
+
+  encode(run) { this.context.addon.encode(run.handle); }
+
+  destroyRun(run) {
+    if (run.handle) this.context.addon.destroyRun(run.handle);
+    run.handle = null;
+  }
+}
+
+module.exports = { DeviceContext, DeviceBuffer, CausalAttentionKernel, MASK };

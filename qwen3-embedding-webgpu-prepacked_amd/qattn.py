@@ -94,6 +94,7 @@ def lib():
         "qattn_qk_norm_rope": (ctypes.c_int, [vp, vp, i64, i64, i32, vp, i32, vp,
                                               ctypes.c_double, ctypes.c_double, vp]),
         "qattn_fill_normal": (ctypes.c_int, [vp, vp, i64, i64, i64, ctypes.c_uint64, vp]),
+        "qattn_fill_token_rows": (ctypes.c_int, [vp, vp, vp, i64, i64, i64, ctypes.c_uint64, vp]),
         "qattn_gen_qkv": (ctypes.c_int, [vp, ctypes.c_uint32, ctypes.c_uint32, vp, i32,
                                          vp, i64, vp, i64, vp, i64, vp]),
         "qattn_event_create": (ctypes.c_int, [vp, pvp]),
@@ -291,6 +292,10 @@ class Context:
     def fill_normal(self, ptr, rows, row_elems, row_stride, seed, stream=None):
         _check(lib().qattn_fill_normal(self.handle, ptr, rows, row_elems, row_stride, seed, stream),
                self.handle)
+
+    def fill_token_rows(self, ptr, ids_ptr, rows, row_elems, row_stride, seed, stream=None):
+        _check(lib().qattn_fill_token_rows(self.handle, ptr, ids_ptr, rows, row_elems, row_stride,
+                                           seed, stream), self.handle)
 
     def gen_qkv(self, config, layer, cu_seqlens, q_ptr, k_ptr, v_ptr, q_row_stride=HQ * HD,
                 k_row_stride=HKV * HD, v_row_stride=HKV * HD, stream=None):

@@ -1,0 +1,132 @@
+'use strict';
+// GPU tests of the Node path: engine -> HipAttentionRuntime -> N-API -> libqattn.so on gfx950.
+// Usage: node gpu.test.js <workdir>   (workdir holds the inputs written by tests/test_gpu_js.py)
+const assert = require('assert');
+const fs = require('fs');
+const path = require('path');
+const pkg = require(path.join(__dirname, '..', '..', 'qwen3-embedding-webgpu-prepacked_amd', 'js'));
+const { Qwen3EmbeddingEngine, HipAttentionRuntime, DeviceContext, CausalAttentionKernel } = pkg;
+
+const work = process.argv[2];
+const cases = [];
+function test(name, fn) { cases.push({ name, fn }); }
+function readU16(file) { const b = fs.readFileSync(file); return new Uint16Array(b.buffer, b.byteOffset, b.length / 2); }
+function readI32(file) { const b = fs.readFileSync(file); return new Int32Array(b.buffer, b.byteOffset, b.length / 4); }
+
+let ctx;
+
+test('device is gfx950', () => {
+  ctx = new DeviceContext(0);
+  const info = ctx.info();
+  console.log('  device', info.name, info.computeUnits);
+  assert.ok(info.name.startsWith('gfx950'));
+});
+
+test('varlen operator through N-API on oracle inputs (output checked in Python)', async () => {
+  const q = readU16(path.join(work, 'q.bin')), k = readU16(path.join(work, 'k.bin')), v = readU16(path.join(work, 'v.bin'));
+  const cu = readI32(path.join(work, 'cu.bin'));
+  const T = cu[cu.length - 1];
+  const bq = ctx.alloc(q.byteLength), bk = ctx.alloc(k.byteLength), bv = ctx.alloc(v.byteLength), bo = ctx.alloc(T * 4096), bl = ctx.alloc((cu.length - 1) * 4096);
+  bq.write(q); bk.write(k); bv.write(v);
+  const attention = new CausalAttentionKernel(ctx);
+  const run = attention.createVarlenRun(bq, bk, bv, bo, cu, { lastRows: bl });
+  assert.strictEqual(run.info.tokens, T);
+  attention.encode(run);
+  await ctx.synchronizeAsync();
+  const o = bo.read(new Uint16Array(T * 2048));
+  fs.writeFileSync(path.join(work, 'o.bin'), Buffer.from(o.buffer));
+  const last = bl.read(new Uint16Array((cu.length - 1) * 2048));
+  for (let s = 0; s < cu.length - 1; s += 1) {
+    const row = cu[s + 1] - 1;
+    for (let d = 0; d < 2048; d += 1) assert.strictEqual(last[s * 2048 + d], o[row * 2048 + d]);
+  }
+  attention.destroyRun(run);
+  for (const b of [bq, bk, bv, bo, bl]) b.destroy();
+});
+
+test('padded createRun (reference layout) equals the varlen run on valid rows', async () => {
+  const q = readU16(path.join(work, 'q.bin')), k = readU16(path.join(work, 'k.bin')), v = readU16(path.join(work, 'v.bin'));
+  const cu = readI32(path.join(work, 'cu.bin'));
+  const o = readU16(path.join(work, 'o.bin'));
+  const batch = cu.length - 1;
+  let S = 0;
+  for (let s = 0; s < batch; s += 1) S = Math.max(S, cu[s + 1] - cu[s]);
+  const qp = new Uint16Array(batch * S * 2048), kp = new Uint16Array(batch * S * 1024), vp = new Uint16Array(batch * S * 1024);
+  for (let s = 0; s < batch; s += 1) {
+    qp.set(q.subarray(cu[s] * 2048, cu[s + 1] * 2048), s * S * 2048);
+    kp.set(k.subarray(cu[s] * 1024, cu[s + 1] * 1024), s * S * 1024);
+    vp.set(v.subarray(cu[s] * 1024, cu[s + 1] * 1024), s * S * 1024);
+  }
+  const bq = ctx.alloc(qp.byteLength), bk = ctx.alloc(kp.byteLength), bv = ctx.alloc(vp.byteLength), bo = ctx.alloc(batch * S * 4096);
+  bq.write(qp); bk.write(kp); bv.write(vp);
+  const attention = new CausalAttentionKernel(ctx);
+  const run = attention.createRun(bq, bk, bv, bo, batch, S);
+  attention.encode(run);
+  await ctx.synchronizeAsync();
+  const op = bo.read(new Uint16Array(batch * S * 2048));
+  for (let s = 0; s < batch; s += 1) {
+    const n = (cu[s + 1] - cu[s]) * 2048;
+    assert.deepStrictEqual(op.subarray(s * S * 2048, s * S * 2048 + n), o.subarray(cu[s] * 2048, cu[s] * 2048 + n));
+  }
+  attention.destroyRun(run);
+  for (const b of [bq, bk, bv, bo]) b.destroy();
+});
+
+test('device mask check through N-API equals the host evaluation', () => {
+  for (const L of [50, 609, 1500]) {
+    const dev = ctx.addon.debugMask(ctx.handle, L, 1, 176, 432);
+    const host = ctx.addon.planMask(L, 1, 176, 432);
+    assert.deepStrictEqual(dev, host);
+  }
+});
+
+test('engine.embed() end to end: unit vectors; a request alone equals the same request in a batch of 16', async () => {
+  const runtime = new HipAttentionRuntime({ context: ctx, layers: 3 });
+  const tokenizer = (text) => ({ input_ids: { tolist: () => [text.split(' ').map((w) => w.length * 131 + w.charCodeAt(0))] } });
+  const engine = new Qwen3EmbeddingEngine(runtime, tokenizer);
+  const texts = Array.from({ length: 16 }, (_, i) => Array.from({ length: 5 + 37 * i }, (_, j) => `w${(i * 7 + j * 13) % 97}x`).join(' '));
+  const batch = await Promise.all(texts.map((t) => engine.embed(t)));
+  for (const e of batch) {
+    assert.strictEqual(e.length, 2048);
+    let norm = 0;
+    for (const x of e) { assert.ok(Number.isFinite(x)); norm += x * x; }
+    assert.ok(Math.abs(Math.sqrt(norm) - 1) < 1e-5);
+  }
+  for (const i of [0, 7, 15]) {
+    const alone = await engine.embed(texts[i]);
+    let dot = 0;
+    for (let d = 0; d < 2048; d += 1) dot += alone[d] * batch[i][d];
+    assert.ok(dot > 0.99999, `batch-vs-single cosine ${dot}`);
+    assert.deepStrictEqual(Array.from(alone), Array.from(batch[i]));
+  }
+  const a = await engine.embed('alpha beta gamma'), b = await engine.embed('alpha beta delta');
+  let dot = 0;
+  for (let d = 0; d < 2048; d += 1) dot += a[d] * b[d];
+  assert.ok(dot < 0.999, 'different token ids give different outputs');
+  for (const p of runtime.plans) p.destroy();
+  runtime.plans = [];
+});
+
+test('plan.run rejects malformed input before launching', async () => {
+  const runtime = new HipAttentionRuntime({ context: ctx, layers: 1 });
+  const plan = runtime.createPlan(2, 4);
+  await assert.rejects(plan.run(new Uint32Array(9), new Uint32Array([4, 5])), /does not match/);
+  await assert.rejects(plan.run(new Uint32Array(3), new Uint32Array([3])), /lengths do not match/);
+  plan.destroy();
+});
+
+(async () => {
+  let failed = 0;
+  for (const c of cases) {
+    try {
+      await c.fn();
+      console.log(`ok - ${c.name}`);
+    } catch (error) {
+      failed += 1;
+      console.log(`not ok - ${c.name}\n  ${error && error.stack}`);
+    }
+  }
+  if (ctx) ctx.destroy();
+  console.log(`${cases.length - failed}/${cases.length} passed`);
+  process.exit(failed ? 1 : 0);
+})();

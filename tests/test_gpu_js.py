@@ -1,0 +1,35 @@
+"""GPU tests of the Node path (engine -> runtime -> N-API -> libqattn.so) under `node`.
+
+The operator parity case feeds oracle-generated inputs through the N-API addon and checks the
+output here against the f64 oracle with the same bar as the C-ABI parity tests.
+"""
+import os
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+@pytest.mark.skipif(shutil.which("node") is None, reason="node is not installed")
+def test_node_gpu_path(oracle, tmp_path):
+    lengths = [33, 150, 1, 64, 97]
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    q, k, v = oracle.gen_qkv(1, 5, cu)
+    for name, arr in (("q", q), ("k", k), ("v", v), ("cu", cu)):
+        arr.tofile(str(tmp_path / f"{name}.bin"))
+    r = subprocess.run(["node", os.path.join(HERE, "js", "gpu.test.js"), str(tmp_path)],
+                       capture_output=True, text=True, timeout=180,
+                       env=dict(os.environ, QATTN_EXPECT_GPU="1"))
+    print(r.stdout, r.stderr[-2000:])
+    assert r.returncode == 0, r.stdout + r.stderr
+    o = np.fromfile(str(tmp_path / "o.bin"), dtype=np.uint16).view(np.float16).astype(np.float64)
+    exact = oracle.attention_exact(q, k, v, cu)
+    o = o.reshape(exact.shape)
+    err = np.abs(o - exact).max()
+    cos = ((o * exact).sum(-1) / (np.linalg.norm(o, axis=-1) * np.linalg.norm(exact, axis=-1))).min()
+    print(f"node path: max|err| {err:.3e} min cos {cos:.7f}")
+    assert err <= 2e-3 and cos >= 0.9999
