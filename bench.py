@@ -136,6 +136,21 @@ def cpu_baseline(selected):
     }
 
 
+def copy_calibration(mib):
+    """Five copies of `mib` MiB between two device buffers: each dispatch reads and writes exactly
+    mib MiB, so a profiler's per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) divided by 1024*mib is the
+    counter's scale for a plain streaming kernel."""
+    import torch
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copy calibration: 5 x {mib} MiB device copies done")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -143,7 +158,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", choices=sorted(SETS), default="both")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run 5 plain device copies of MIB MiB (torch copy_) and exit: the "
+                         "known-size reference for rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each GPU box has one "
               "MI355X). Run with --gpus 1.", file=sys.stderr)

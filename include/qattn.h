@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define QATTN_ABI_VERSION 1
+#define QATTN_ABI_VERSION 2
 
 #define QATTN_Q_HEADS 16
 #define QATTN_KV_HEADS 8
@@ -105,8 +105,9 @@ typedef struct qattn_run_desc {
   void* o_last;
 } qattn_run_desc;
 
-/* Plans the launch (validates, builds the work list of (sequence, kv_head, query block) items
- * heaviest first, uploads it) and returns a run that owns its device work list. */
+/* Plans the launch (validates, builds the work list of (sequence, kv_head, query block) items,
+ * spreads it over persistent workgroups -- "slots", two per compute unit -- longest first with
+ * each KV head's items on one XCD, uploads it) and returns a run that owns its device work list. */
 int qattn_run_create(qattn_ctx* ctx, const qattn_run_desc* desc, qattn_run** out);
 /* Enqueues the attention kernel of a run on `stream` (NULL: the context stream). */
 int qattn_run_encode(qattn_run* run, qattn_stream_t stream);
@@ -120,19 +121,29 @@ typedef struct qattn_run_info {
   int64_t pairs;            /* retained (query, key) pairs summed over sequences */
   int64_t flops;            /* 4 * 128 * 16 * pairs: QK^T and PV over all query heads */
   int64_t bytes;            /* 12288 * tokens (+ 4096 per sequence with o_last): Q,K,V,O fp16 */
-  int32_t work_items;       /* workgroups launched */
+  int32_t work_items;       /* (sequence, kv_head, 64-query block) items */
   int32_t block_queries;    /* query positions per work item */
   int64_t tile_pairs;       /* (query, key) pairs inside the MFMA tiles computed, per query head */
+  int32_t slots;            /* persistent workgroups launched (each runs a list of items) */
+  int32_t reserved;
 } qattn_run_info;
 int qattn_run_get_info(const qattn_run* run, qattn_run_info* info);
 
 /* Host-only planning (no device needed): validates `desc` exactly as qattn_run_create does and
- * reports the work list a run would launch, in launch order.  Each item is four int32:
+ * reports the work list a run on an MI355X (256 compute units, 512 slots) would upload: items
+ * grouped by slot, heaviest first within a slot.  Each item is four int32:
  * {first token of the sequence, sequence length, query block, sequence<<4 | kv_head}.
  * `items` may be NULL (count only); `*count` receives the number of items, `info` (optional) the
- * run's figures.  Fails with QATTN_EINVAL if `capacity` is too small for a non-NULL `items`. */
+ * run's figures.  Fails with QATTN_EINVAL if `capacity` is too small for a non-NULL `items`.
+ * Replaces the reference's dispatch-size computation (ops.ts:329-343). */
 int qattn_plan_describe(const qattn_run_desc* desc, int32_t* items, int32_t capacity,
                         int32_t* count, qattn_run_info* info);
+/* The slot structure of the same plan for at most `max_slots` workgroups (<= 0: 512): slot b
+ * runs items slot_begin[b] .. slot_begin[b+1]-1 of qattn_plan_describe's list and is dispatched
+ * to XCD b % 8.  `*nslots` receives the slot count; `slot_begin` (optional, `capacity` >=
+ * nslots + 1 entries) the offsets. */
+int qattn_plan_slots(const qattn_run_desc* desc, int32_t max_slots, int32_t* slot_begin,
+                     int32_t capacity, int32_t* nslots);
 
 /* One-shot: create, encode, wait for completion, destroy. */
 int qattn_prefill(qattn_ctx* ctx, const qattn_run_desc* desc, qattn_stream_t stream);

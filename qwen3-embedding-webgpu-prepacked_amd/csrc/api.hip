@@ -33,7 +33,8 @@ struct AttnParams {
   half_t* o_last;
   int64_t q_stride, k_stride, v_stride, o_stride;
   const WorkItem* work;
-  int32_t n_work;
+  const int32_t* slot_begin;
+  int32_t n_slots;
   MaskSpec mask;
   float scale_log2;
 };
@@ -54,6 +55,7 @@ using namespace qattn;
 
 struct qattn_ctx {
   int device = 0;
+  int cu_count = 0;
   hipStream_t stream = nullptr;
   std::string last_error;
   std::mutex mu;
@@ -62,7 +64,7 @@ struct qattn_ctx {
 struct qattn_run {
   qattn_ctx* ctx = nullptr;
   AttnParams params{};
-  WorkItem* work_dev = nullptr;
+  void* plan_dev = nullptr;  // work items by slot, then the slot offsets
   int64_t v_offset = 0;
   bool has_o_last = false;
   qattn_run_info info{};
@@ -151,11 +153,13 @@ int validate_desc(qattn_ctx* ctx, const qattn_run_desc* d) {
   if (rc) return rc;
   const int64_t T = d->cu_seqlens[d->nseq];
   if (T >= ((int64_t)1 << 31)) return fail(ctx, QATTN_EINVAL, "too many tokens (%lld)", (long long)T);
-  // The kernel addresses one sequence's rows with 32-bit byte offsets.
-  const int64_t max_stride = std::max(std::max(d->q_row_stride, d->k_row_stride), d->v_row_stride);
+  // The kernel addresses one sequence's rows (plus up to one 64-row tile past its end, which the
+  // buffer range check zero-fills) with 32-bit byte offsets.
+  const int64_t max_stride = std::max(std::max(d->q_row_stride, d->k_row_stride),
+                                      std::max(d->v_row_stride, d->o_row_stride));
   for (int32_t s = 0; s < d->nseq; ++s) {
     const int64_t L = d->cu_seqlens[s + 1] - d->cu_seqlens[s];
-    if (L * max_stride * 2 >= ((int64_t)1 << 31))
+    if ((L + kTileK) * max_stride * 2 >= ((int64_t)1 << 31))
       return fail(ctx, QATTN_EINVAL, "sequence %d: %lld tokens x row stride %lld exceeds 2 GiB", s,
                   (long long)L, (long long)max_stride);
   }
@@ -205,6 +209,7 @@ int qattn_create(int device, qattn_ctx** out) {
   auto* ctx = new (std::nothrow) qattn_ctx();
   if (!ctx) return fail(nullptr, QATTN_ENOMEM, "out of host memory");
   ctx->device = device;
+  ctx->cu_count = prop.multiProcessorCount;
   DeviceGuard g(device);
   e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
@@ -301,18 +306,35 @@ int qattn_buffer_fill_u16(qattn_ctx* ctx, void* dst, uint16_t value, size_t coun
 
 namespace {
 
-// The planner: validated description -> work items in launch order + run figures.
-int plan_work(qattn_ctx* ctx, const qattn_run_desc* d, std::vector<WorkItem>* out,
+// Slots: persistent workgroups of one launch.  Two fit on a CU (64 KiB LDS, <= 256 VGPRs each);
+// workgroup b is dispatched to XCD b % kXcds, so the planner puts every item of KV head g on
+// slots b = kXcds * j + g % kXcds and that head's K/V tiles stay in one XCD's L2.
+constexpr int kXcds = 8;
+constexpr int kBlocksPerCU = 2;
+constexpr int kDefaultSlots = 256 * kBlocksPerCU;  // MI355X: 256 CUs
+
+struct Plan {
+  std::vector<WorkItem> items;       // grouped by slot, heaviest first within a slot
+  std::vector<int32_t> slot_begin;   // n_slots + 1 offsets into items
+};
+
+// Relative cost of a work item for load balancing: its key tiles plus a fixed share for the
+// item's start (Q and first tiles) and end (last PV, O stores) that the pipeline cannot hide.
+int item_cost(int ntiles) { return 4 * ntiles + 3; }
+
+// The planner: validated description -> work items grouped into slots + run figures.
+int plan_work(qattn_ctx* ctx, const qattn_run_desc* d, int max_slots, Plan* out,
               qattn_run_info* info_out, MaskSpec* mask_out) {
   int rc = validate_desc(ctx, d);
   if (rc) return rc;
+  if (max_slots < kXcds) max_slots = kXcds;
   const MaskSpec mask{d->mask, d->mask == QATTN_MASK_PREFIX_LOCAL ? d->prefix : 0,
                       d->mask == QATTN_MASK_PREFIX_LOCAL ? d->window : 0};
   struct Item {
     WorkItem w;
     int cost;
   };
-  std::vector<Item> items;
+  std::vector<Item> group_items[kXcds];
   qattn_run_info info{};
   info.block_queries = kBlockQ;
   for (int32_t s = 0; s < d->nseq; ++s) {
@@ -325,20 +347,41 @@ int plan_work(qattn_ctx* ctx, const qattn_run_desc* d, std::vector<WorkItem>* ou
       const TileRanges tr = key_tiles(q0, q1, L, mask);
       // MFMA tile work of one query head: the wavefronts holding rows [q0, q0+31] and
       // [q0+32, q0+63] each compute every tile of the work item.
-      const int cost = tr.count() * (q0 + kWaveQ < L ? 2 : 1);
-      info.tile_pairs += (int64_t)cost * kWaveQ * kTileK;
+      info.tile_pairs += (int64_t)tr.count() * (q0 + kWaveQ < L ? 2 : 1) * kWaveQ * kTileK;
       for (int g = 0; g < kKVHeads; ++g)
-        items.push_back({WorkItem{start, L, qb, (s << 4) | g}, tr.count() * 256 + cost});
+        group_items[g % kXcds].push_back({WorkItem{start, L, qb, (s << 4) | g}, item_cost(tr.count())});
     }
   }
-  // Heaviest first: most key tiles walked, then most wavefront tiles computed; stable so
-  // equal items keep sequence/head order.
-  std::stable_sort(items.begin(), items.end(), [](const Item& a, const Item& b) { return a.cost > b.cost; });
-  info.work_items = (int32_t)items.size();
+  // Longest processing time first, per XCD group: items in falling cost (stable, so equal items
+  // keep sequence order) each go to the least loaded of the group's slots.
+  const int per_group = max_slots / kXcds;
+  std::vector<std::vector<int>> lists[kXcds];
+  int used = 0;
+  for (int g = 0; g < kXcds; ++g) {
+    auto& items = group_items[g];
+    std::stable_sort(items.begin(), items.end(), [](const Item& a, const Item& b) { return a.cost > b.cost; });
+    const int m = std::min<int>(per_group, (int)items.size());
+    lists[g].assign(m, {});
+    std::vector<int64_t> load(m, 0);
+    for (int i = 0; i < (int)items.size(); ++i) {
+      const int j = (int)(std::min_element(load.begin(), load.end()) - load.begin());
+      lists[g][j].push_back(i);
+      load[j] += items[i].cost;
+    }
+    used = std::max(used, m);
+  }
+  out->items.clear();
+  out->slot_begin.assign(1, 0);
+  for (int j = 0; j < used; ++j)
+    for (int g = 0; g < kXcds; ++g) {
+      if (j < (int)lists[g].size())
+        for (int i : lists[g][j]) out->items.push_back(group_items[g][i].w);
+      out->slot_begin.push_back((int32_t)out->items.size());
+    }
+  info.work_items = (int32_t)out->items.size();
+  info.slots = (int32_t)out->slot_begin.size() - 1;
   info.flops = 4ll * kHeadDim * kQHeads * info.pairs;
   info.bytes = 12288ll * info.tokens + (d->o_last ? 4096ll * d->nseq : 0);
-  out->resize(items.size());
-  for (size_t i = 0; i < items.size(); ++i) (*out)[i] = items[i].w;
   if (info_out) *info_out = info;
   if (mask_out) *mask_out = mask;
   return QATTN_OK;
@@ -351,16 +394,31 @@ extern "C" {
 int qattn_plan_describe(const qattn_run_desc* desc, int32_t* items, int32_t capacity,
                         int32_t* count, qattn_run_info* info) {
   if (!count) return fail(nullptr, QATTN_EINVAL, "count is NULL");
-  std::vector<WorkItem> work;
+  Plan plan;
   qattn_run_info inf{};
-  int rc = plan_work(nullptr, desc, &work, &inf, nullptr);
+  int rc = plan_work(nullptr, desc, kDefaultSlots, &plan, &inf, nullptr);
   if (rc) return rc;
-  *count = (int32_t)work.size();
+  *count = (int32_t)plan.items.size();
   if (info) *info = inf;
   if (items) {
-    if (capacity < (int32_t)work.size())
-      return fail(nullptr, QATTN_EINVAL, "capacity %d < %zu work items", capacity, work.size());
-    std::memcpy(items, work.data(), work.size() * sizeof(WorkItem));
+    if (capacity < (int32_t)plan.items.size())
+      return fail(nullptr, QATTN_EINVAL, "capacity %d < %zu work items", capacity, plan.items.size());
+    std::memcpy(items, plan.items.data(), plan.items.size() * sizeof(WorkItem));
+  }
+  return QATTN_OK;
+}
+
+int qattn_plan_slots(const qattn_run_desc* desc, int32_t max_slots, int32_t* slot_begin,
+                     int32_t capacity, int32_t* nslots) {
+  if (!nslots) return fail(nullptr, QATTN_EINVAL, "nslots is NULL");
+  Plan plan;
+  int rc = plan_work(nullptr, desc, max_slots > 0 ? max_slots : kDefaultSlots, &plan, nullptr, nullptr);
+  if (rc) return rc;
+  *nslots = (int32_t)plan.slot_begin.size() - 1;
+  if (slot_begin) {
+    if (capacity < (int32_t)plan.slot_begin.size())
+      return fail(nullptr, QATTN_EINVAL, "capacity %d < %zu slot offsets", capacity, plan.slot_begin.size());
+    std::memcpy(slot_begin, plan.slot_begin.data(), plan.slot_begin.size() * sizeof(int32_t));
   }
   return QATTN_OK;
 }
@@ -368,10 +426,10 @@ int qattn_plan_describe(const qattn_run_desc* desc, int32_t* items, int32_t capa
 int qattn_run_create(qattn_ctx* ctx, const qattn_run_desc* d, qattn_run** out) {
   if (!ctx || !out) return fail(ctx, QATTN_EINVAL, "ctx/out is NULL");
   *out = nullptr;
-  std::vector<WorkItem> host;
+  Plan plan;
   qattn_run_info info{};
   MaskSpec mask{};
-  int rc = plan_work(ctx, d, &host, &info, &mask);
+  int rc = plan_work(ctx, d, std::max(1, ctx->cu_count) * kBlocksPerCU, &plan, &info, &mask);
   if (rc) return rc;
 
   auto* run = new (std::nothrow) qattn_run();
@@ -380,16 +438,22 @@ int qattn_run_create(qattn_ctx* ctx, const qattn_run_desc* d, qattn_run** out) {
   run->info = info;
   run->v_offset = d->v_offset;
   run->has_o_last = d->o_last != nullptr;
-  if (!host.empty()) {
+  // One upload: the items, then the slot offsets (16-byte items keep the offsets aligned).
+  const size_t items_bytes = plan.items.size() * sizeof(WorkItem);
+  const size_t slots_bytes = plan.slot_begin.size() * sizeof(int32_t);
+  std::vector<char> host(items_bytes + slots_bytes);
+  if (items_bytes) std::memcpy(host.data(), plan.items.data(), items_bytes);
+  std::memcpy(host.data() + items_bytes, plan.slot_begin.data(), slots_bytes);
+  {
     DeviceGuard g(ctx->device);
-    hipError_t e = hipMalloc(&run->work_dev, host.size() * sizeof(WorkItem));
+    hipError_t e = hipMalloc(&run->plan_dev, host.size());
     if (e != hipSuccess) {
       delete run;
       return fail(ctx, QATTN_ENOMEM, "hipMalloc(work list): %s", hipGetErrorString(e));
     }
-    e = hipMemcpy(run->work_dev, host.data(), host.size() * sizeof(WorkItem), hipMemcpyHostToDevice);
+    e = hipMemcpy(run->plan_dev, host.data(), host.size(), hipMemcpyHostToDevice);
     if (e != hipSuccess) {
-      (void)hipFree(run->work_dev);
+      (void)hipFree(run->plan_dev);
       delete run;
       return fail(ctx, QATTN_EHIP, "hipMemcpy(work list): %s", hipGetErrorString(e));
     }
@@ -404,8 +468,9 @@ int qattn_run_create(qattn_ctx* ctx, const qattn_run_desc* d, qattn_run** out) {
   p.k_stride = d->k_row_stride;
   p.v_stride = d->v_row_stride;
   p.o_stride = d->o_row_stride;
-  p.work = run->work_dev;
-  p.n_work = (int32_t)host.size();
+  p.work = static_cast<const WorkItem*>(run->plan_dev);
+  p.slot_begin = reinterpret_cast<const int32_t*>(static_cast<const char*>(run->plan_dev) + items_bytes);
+  p.n_slots = info.slots;
   p.mask = mask;
   p.scale_log2 = (float)(1.4426950408889634 / std::sqrt(128.0));
   *out = run;
@@ -439,10 +504,10 @@ int qattn_run_rebind(qattn_run* run, const void* q, const void* k, const void* v
 
 void qattn_run_destroy(qattn_run* run) {
   if (!run) return;
-  if (run->work_dev) {
+  if (run->plan_dev) {
     DeviceGuard g(run->ctx->device);
     (void)hipStreamSynchronize(run->ctx->stream);
-    (void)hipFree(run->work_dev);
+    (void)hipFree(run->plan_dev);
   }
   delete run;
 }

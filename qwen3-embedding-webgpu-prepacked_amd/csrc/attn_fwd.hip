@@ -3,8 +3,13 @@
 // Replaces the reference's tiled flash attention shader (src/webgpu/ops.ts:168-241).  Same
 // result (softmax(mask(QK^T)/sqrt(128)) V per query head, mask ops.ts:205-209,220), computed
 // the CDNA4 way:
-//   * one workgroup = (sequence, KV head, 64 query positions) and BOTH query heads of the GQA
+//   * a work item = (sequence, KV head, 64 query positions) and BOTH query heads of the GQA
 //     group (4 wavefronts x 32 rows), so each K/V tile is staged in LDS once for two heads;
+//   * persistent workgroups: the host planner gives every workgroup ("slot") a list of work
+//     items, balanced longest-first, and keeps each KV head's items on one XCD (slot b runs on
+//     XCD b % 8) so that head's K/V stays in one L2.  While an item runs its last key tile, the
+//     workgroup already loads the next item's Q and first two K tiles, and it never waits for
+//     an item's O stores: loads, MFMA work and stores of neighbouring items overlap;
 //   * S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_32x32x16_f16 (fp16 in, fp32 accumulate), so
 //     every lane owns one query row: the row max / row sum need one permlane32 swap;
 //   * K/V tiles go HBM -> LDS with buffer_load ... lds (no staging registers); the buffer
@@ -13,9 +18,9 @@
 //     fragment reads (ds_read_b128) and the V^T fragment reads (ds_read_b64_tr_b16, the gfx950
 //     LDS transpose load) are bank-conflict free;
 //   * software pipelined: iteration j issues the S^T MFMAs of tile j+1 and the PV MFMAs of tile
-//     j-1 in the same basic block as the softmax VALU work of tile j, so the matrix cores and
-//     the VALU run side by side; the score / probability registers alternate between two sets
-//     by iteration parity (no copies); K and V are double buffered in LDS;
+//     j-1 in the same basic block as the softmax VALU work of tile j; the score / probability
+//     registers alternate between two sets by iteration parity (no copies); K and V are double
+//     buffered in LDS;
 //   * lazy rescaling: O and l are rescaled only when a row max grows by more than 2^8;
 //   * causal and prefix/local masks skip whole key tiles (key_tiles); element masks run only on
 //     tiles that straddle a boundary (tile_full).
@@ -49,17 +54,33 @@ struct AttnParams {
   half_t* o;
   half_t* o_last;
   int64_t q_stride, k_stride, v_stride, o_stride;
-  const WorkItem* work;
-  int32_t n_work;
+  const WorkItem* work;       // work items grouped by slot
+  const int32_t* slot_begin;  // slot b owns work[slot_begin[b] .. slot_begin[b+1])
+  int32_t n_slots;            // workgroups launched
   MaskSpec mask;
   float scale_log2;  // (1/sqrt(128)) * log2(e)
 };
+
+// Vector-memory instructions per lane that one item's prologue loads (Q: 8 x 16 B, K tiles 0
+// and 1: kLoadsPerTile each) and that one item's epilogue stores (o_last row and O rows, 8 x 16 B
+// each, always issued: out-of-range lanes are dropped by the buffer resource).  The s_waitcnt
+// counts below rely on these being exact; vector memory operations retire in issue order.
+constexpr int kPrefetchOps = 8 + 2 * kLoadsPerTile;
+constexpr int kStoreOps = 16;
+
+// s_waitcnt vmcnt(N) only (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
 
 __device__ inline f16x mfma32(h8 a, h8 b, f16x c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-// Raw buffer resource over `bytes` bytes at `base`; loads past the end return zeros.
+// Raw buffer resource over `bytes` bytes at `base`; loads past the end return zeros and stores
+// past the end are dropped.
 __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
 }
@@ -77,6 +98,11 @@ __device__ inline float pair_sum(float x) {
 // Offset of S^T accumulator element r (0..31 over the two 32-key blocks) from kb + 4*hl.
 __device__ constexpr int key_off(int r) { return 32 * (r >> 4) + 8 * ((r & 15) >> 2) + (r & 3); }
 
+__device__ inline uint32_t pack2(float a, float b) {
+  const h2 v = {(half_t)a, (half_t)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   // K and V tiles, double buffered, 16 KiB each.  Four distinct objects (not offsets into one
   // array) with buffer choices fixed at compile time, so the compiler can see that the LDS-DMA
@@ -86,90 +112,116 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   __shared__ __attribute__((aligned(1024))) char sV0[kTileBytes];
   __shared__ __attribute__((aligned(1024))) char sV1[kTileBytes];
 
-  const WorkItem w = p.work[blockIdx.x];
-  const int seq_start = w.seq_start;
-  const int S = w.seq_len;
-  const int kvh = w.seq_kvh & 15;
-  const int seq = w.seq_kvh >> 4;
+  // The work list is read-only for the whole launch: read it through the constant address
+  // space so item loads are scalar loads, which no vector-memory wait (for the O stores) covers.
+  typedef __attribute__((address_space(4))) const int32_t const_i32_t;
+  const_i32_t* const work_words = (const_i32_t*)p.work;
+  auto work = [&](int i) {
+    const_i32_t* w = work_words + 4 * i;
+    return WorkItem{w[0], w[1], w[2], w[3]};
+  };
+  const int i_begin = ((const_i32_t*)p.slot_begin)[blockIdx.x];
+  const int i_end = ((const_i32_t*)p.slot_begin)[blockIdx.x + 1];
+  if (i_begin >= i_end) return;
+
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps rsrc/M0 in SGPRs
   const int lane = tid & 63;
   const int lq = lane & 31;  // query row of this lane inside the wave's 32-row tile
   const int hl = lane >> 5;  // which half of the MFMA K dimension this lane feeds
-  const int head = kvh * kGroup + (wave >> 1);
-  const int blk_q0 = w.q_block * kBlockQ;
-  const int blk_q1 = min(S, blk_q0 + kBlockQ) - 1;
-  const int wq0 = blk_q0 + (wave & 1) * kWaveQ;
-  const int wq1 = min(S - 1, wq0 + kWaveQ - 1);
-  const int q_pos = wq0 + lq;
+  const int head_in_group = wave >> 1;
+  const int wave_q = (wave & 1) * kWaveQ;
   const MaskSpec mask = p.mask;
-  const int ps = min(S, mask.prefix);
-  const int ws = min(S, mask.window);
   const float c = p.scale_log2;
-
-  // ---- Q fragment (B operand of S^T = K Q^T): lane = query row, 8 consecutive dims per step.
-  h8 qreg[8];
-  {
-    const half_t* qhead = p.q + (int64_t)seq_start * p.q_stride + head * kHeadDim;
-    const auto rs = make_rsrc(qhead, (uint32_t)S * (uint32_t)p.q_stride * 2u);
-    const uint32_t row_off = (uint32_t)q_pos * (uint32_t)p.q_stride * 2u + 16u * hl;
-#pragma unroll
-    for (int st = 0; st < 8; ++st)
-      qreg[st] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(rs, row_off + 32u * st, 0, 0));
-  }
+  const uint32_t qstride_b = (uint32_t)p.q_stride * 2u, ostride_b = (uint32_t)p.o_stride * 2u;
+  const uint32_t kstride_b = (uint32_t)p.k_stride * 2u, vstride_b = (uint32_t)p.v_stride * 2u;
 
   // ---- tile loads: kLoadsPerTile buffer_load...lds per lane per tile; instruction j of wave
   // `wave` fills LDS rows 16j + 4*wave .. +3 (1 KiB, lane-contiguous).  Lane writes physical chunk
   // lane&15 of row r with the logical 16 B chunk (lane&15) ^ swizzle(r) of key row kb + r.
-  const char* kbase = reinterpret_cast<const char*>(p.k + (int64_t)seq_start * p.k_stride + kvh * kHeadDim);
-  const char* vbase = reinterpret_cast<const char*>(p.v + (int64_t)seq_start * p.v_stride + kvh * kHeadDim);
-  const uint32_t kstride_b = (uint32_t)p.k_stride * 2u, vstride_b = (uint32_t)p.v_stride * 2u;
-  uint32_t koff[kLoadsPerTile], voff[kLoadsPerTile];
-#pragma unroll
-  for (int j = 0; j < kLoadsPerTile; ++j) {
-    const int r = 16 * j + 4 * wave + (lane >> 4);
-    const int pc = lane & 15;
-    koff[j] = (uint32_t)r * kstride_b + (uint32_t)((pc ^ (r & 15)) << 4);
-    voff[j] = (uint32_t)r * vstride_b + (uint32_t)((pc ^ ((r & 3) << 1)) << 4);
-  }
-  auto load_tile = [&](char* dst, const char* base, uint32_t stride_b, const uint32_t* off, int kt) {
+  // Row r = 16j + r0 with r0 = 4*wave + lane/16, so r & 15 = r0: the swizzle is the same for
+  // every j and instruction j only adds 16j rows.  That step goes into the VGPR offset (one add),
+  // not the SGPR offset, because the buffer range check that zero-fills rows past the sequence
+  // covers the VGPR and immediate offsets only.
+  const int r0 = 4 * wave + (lane >> 4), pc = lane & 15;
+  const uint32_t koff = (uint32_t)r0 * kstride_b + (uint32_t)((pc ^ r0) << 4);
+  const uint32_t voff = (uint32_t)r0 * vstride_b + (uint32_t)((pc ^ ((r0 & 3) << 2)) << 4);
+  // Key tile `kt` of a sequence of S rows starting at `base` (kt * kTileK < S always).
+  auto load_tile = [&](char* dst, const char* base, uint32_t stride_b, uint32_t off, int kt, int S) {
     const int kb = kt * kTileK;
     const auto rs = make_rsrc(base + (int64_t)kb * stride_b, (uint32_t)(S - kb) * stride_b);
 #pragma unroll
-    for (int j = 0; j < kLoadsPerTile; ++j)
+    for (int j = 0; j < kLoadsPerTile; ++j) {
+      // The add stays here (not hoisted into four loop-invariant registers).
+      uint32_t step = (uint32_t)(16 * j) * stride_b;
+      asm volatile("" : "+s"(step));
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(dst + j * 4096 + wave * 1024), 16,
-                                               off[j], 0, 0, 0);
+                                               off + step, 0, 0, 0);
+    }
   };
 
   // ---- LDS read addresses.
   // K (A operand of S^T): lane reads key row lq (+32 for the second block), logical chunk
-  // 2*st + hl, stored at physical chunk (2*st + hl) ^ (lq & 15).
-  uint32_t kread[8];
-#pragma unroll
-  for (int st = 0; st < 8; ++st) kread[st] = lq * kRowBytes + (((2 * st + hl) ^ (lq & 15)) << 4);
+  // 2*st + hl, stored at physical chunk (2*st + hl) ^ (lq & 15).  Bit 0 of that chunk is
+  // hl ^ lq, bits 3:1 are st ^ ((lq & 15) >> 1), so the byte address is
+  // kread_base + ((st << 5) ^ kread_xor): one v_xad_u32 per step instead of 8 live registers.
+  const uint32_t kread_base = lq * kRowBytes + (((hl ^ lq) & 1) << 4);
+  const uint32_t kread_xor = ((lq & 15) >> 1) << 5;
   // V^T (A operand of O^T = V^T P^T) through ds_read_b64_tr_b16: in each 16-lane group G the
   // source lane a reads 4 halves at key row 4*(G>>1) + (a>>2) (+16t, +8 for slots 4..7), dims
-  // 32db + 16(G&1) + 4(a&3); lane a then receives V[4 keys][dim 32db + 16(G&1) + a].
+  // 32db + 16(G&1) + 4(a&3); lane a then receives V[4 keys][dim 32db + 16(G&1) + a].  V rows are
+  // stored with physical chunk = logical chunk ^ ((row & 3) << 2): the 32 lanes the LDS serves
+  // per pass read rows 4i..4i+3 x the 4 chunks of dims 32db..32db+31, and the swizzle spreads
+  // them over all 16 chunks = all 64 banks.
   uint32_t vread[4];
   {
     const int a = lane & 15, G = lane >> 4;
     const int row = 4 * (G >> 1) + (a >> 2);
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      const int chunk = (4 * db + 2 * (G & 1) + ((a & 3) >> 1)) ^ ((a >> 2) << 1);
+      const int chunk = (4 * db + 2 * (G & 1) + ((a & 3) >> 1)) ^ ((a >> 2) << 2);
       vread[db] = row * kRowBytes + (chunk << 4) + ((a & 1) << 3);
     }
   }
+
+  // ---- Q fragment (B operand of S^T = K Q^T): lane = query row, 8 consecutive dims per step.
+  h8 qreg[8];
+
+  // The loads that start a work item: this wave's Q rows into qreg, K tiles 0 and 1 into sK0 /
+  // sK1 (tile 0 twice for a one-tile item, so the instruction count never varies).  Exactly
+  // kPrefetchOps vector-memory instructions per lane.
+  auto start_loads = [&](const WorkItem& w) {
+    const int S = w.seq_len, kvh = w.seq_kvh & 15, q0 = w.q_block * kBlockQ;
+    const TileRanges t = key_tiles(q0, min(S, q0 + kBlockQ) - 1, S, mask);
+    const half_t* qhead = p.q + (int64_t)w.seq_start * p.q_stride + (kvh * kGroup + head_in_group) * kHeadDim;
+    const auto rs = make_rsrc(qhead, (uint32_t)S * qstride_b);
+    const uint32_t row_off = (uint32_t)(q0 + wave_q + lq) * qstride_b + 16u * hl;
+#pragma unroll
+    for (int st = 0; st < 8; ++st)
+      qreg[st] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(rs, row_off + 32u * st, 0, 0));
+    const char* kb = reinterpret_cast<const char*>(p.k + (int64_t)w.seq_start * p.k_stride + kvh * kHeadDim);
+    load_tile(sK0, kb, kstride_b, koff, t.at(0), S);
+    load_tile(sK1, kb, kstride_b, koff, t.at(t.count() > 1 ? 1 : 0), S);
+  };
+
+  // ---- per-item state (uniform over the workgroup except q_pos)
+  int seq_start = 0, S = 1, kvh = 0, seq = 0, wq0 = 0, wq1 = 0, q_pos = 0, ps = 0, ws = 0, ntiles = 0;
+  TileRanges tiles{};
+  const char* kbase = nullptr;
+  const char* vbase = nullptr;
 
   // S^T (64 keys x 32 queries) for the K tile in `kt`.  Lane holds S^T[key][q_pos] for
   // key = kb + 4*hl + key_off(r), r = 0..31 over (s[0], s[1]).
   auto qk = [&](const char* kt, f16x (&s)[2]) {
     s[0] = f16x{};
     s[1] = f16x{};
+    uint32_t kx = kread_xor;
+    asm volatile("" : "+v"(kx));  // keeps the 8 addresses from being hoisted into registers
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
-      const h8 a0 = *reinterpret_cast<const h8*>(kt + kread[st]);
-      const h8 a1 = *reinterpret_cast<const h8*>(kt + kread[st] + 32 * kRowBytes);
+      const uint32_t ka = kread_base + (((uint32_t)st << 5) ^ kx);
+      const h8 a0 = *reinterpret_cast<const h8*>(kt + ka);
+      const h8 a1 = *reinterpret_cast<const h8*>(kt + ka + 32 * kRowBytes);
       s[0] = mfma32(a0, qreg[st], s[0]);
       s[1] = mfma32(a1, qreg[st], s[1]);
     }
@@ -178,15 +230,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   // O^T (128 d x 32 q) += V^T (128 x 64 keys) . P^T.  Step t covers keys kb+16t..kb+16t+15;
   // slot j of lane half hl is key 16t + 8*(j>>2) + 4*hl + (j&3), whose probability is pf[t][j].
   f16x o[4];
-#pragma unroll
-  for (int db = 0; db < 4; ++db) o[db] = f16x{};
   auto pv = [&](const char* vt, const h8 (&pf)[4]) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t*)(vt + vread[db] + t * 4096));
-        const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t*)(vt + vread[db] + t * 4096 + 2048));
+        const char* vp = vt + vread[db] + t * 4096;
+        const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t*)vp);
+        const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t*)(vp + 2048));
         const h4 lo_h = __builtin_bit_cast(h4, lo), hi_h = __builtin_bit_cast(h4, hi);
         const h8 va = {lo_h[0], lo_h[1], lo_h[2], lo_h[3], hi_h[0], hi_h[1], hi_h[2], hi_h[3]};
         o[db] = mfma32(va, pf[t], o[db]);
@@ -194,12 +245,36 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     }
   };
 
-  // Element mask of a boundary tile (keys that keep_key() drops become -inf).
+  // Element mask of a boundary tile: the keys keep_key() drops become -inf.  With
+  // o = key_off(r) = key - kl (kl = kb + 4 hl), keep_key is
+  //   o <= d1  &&  (o < pe  ||  o >= d2),   d1 = q_pos - kl, pe = ps - kl, d2 = d1 - ws + 1,
+  // compares of compile-time offsets against per-lane thresholds.  The tile's position (uniform)
+  // decides which compares can fail, so most tiles need one compare + one select per element:
+  //   * every key in the prefix or in every row's window (all diagonal tiles, every tile of
+  //     the causal kind): only o <= d1;
+  //   * beyond the prefix and left of every row (a window-start tile): only o >= d2;
+  //   * left of every row's window (the prefix's last, partial tile): only o < pe.
   auto apply_mask = [&](f16x (&s)[2], int kb) {
     const int kl = kb + 4 * hl;
+    const int d1 = q_pos - kl;
+    const int ke = kb + kTileK - 1;
+    auto drop_if = [&](auto pred) {
 #pragma unroll
-    for (int r = 0; r < 32; ++r)
-      if (!keep_key(q_pos, kl + key_off(r), ps, ws, mask.kind)) s[r >> 4][r & 15] = -INFINITY;
+      for (int r = 0; r < 32; ++r) s[r >> 4][r & 15] = pred(key_off(r)) ? -INFINITY : s[r >> 4][r & 15];
+    };
+    if (mask.kind == 0 || ke < ps || kb >= wq1 - ws + 1) {
+      drop_if([&](int o) { return o > d1; });
+    } else if (kb >= ps && ke <= wq0) {
+      const int d2 = d1 - ws + 1;
+      drop_if([&](int o) { return o < d2; });
+    } else if (ke < wq0 - ws + 1) {
+      const int pe = ps - kl;
+      drop_if([&](int o) { return o >= pe; });
+    } else {
+      const int pe = ps - kl, d2 = d1 - ws + 1;
+      // bitwise, not short-circuit: one select per element instead of a branch
+      drop_if([&](int o) { return (o > d1) | ((o >= pe) & (o < d2)); });
+    }
   };
 
   // Online softmax of this lane's row over one tile's 64 scores -> fp16 P; returns whether the
@@ -246,40 +321,47 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     }
   };
 
-  const TileRanges tiles = key_tiles(blk_q0, blk_q1, S, mask);
-  const int ntiles = tiles.count();
-
   // Two register sets for scores / probabilities, alternating by iteration parity.
   f16x sA[2], sB[2];
   h8 pA[4], pB[4];
 
-  // Prologue: K(0), K(1) resident; S(0) computed.
-  load_tile(sK0, kbase, kstride_b, koff, tiles.at(0));
-  if (ntiles > 1) load_tile(sK1, kbase, kstride_b, koff, tiles.at(1));
-  __builtin_amdgcn_s_waitcnt(0);  // (gfx9 encoding 0: vmcnt/expcnt/lgkmcnt all zero)
-  __syncthreads();
-  qk(sK0, sA);
-
-  // Iteration `it`, B = it & 1 (compile time).  Before it: S(it) in s_cur, P(it-1) in p_prev,
-  // K(it+1) in sK<B^1>, V(it-1) in sV<B^1>.  It refills sK<B> with K(it+2) and sV<B> with V(it),
-  // computes S(it+1) into s_nxt (stale-buffer garbage on the last tile, never used), adds
-  // P(it-1) V(it-1) to O and turns S(it) into P(it) in p_cur.
+  // Iteration `it` of the current item, B = it & 1 (compile time).  Before it: S(it) in s_cur,
+  // P(it-1) in p_prev, K(it+1) in sK<B^1>, V(it-1) in sV<B^1>.  It refills sK<B> with K(it+2) and
+  // sV<B> with V(it), computes S(it+1) into s_nxt, adds P(it-1) V(it-1) to O and turns S(it)
+  // into P(it) in p_cur.  The LAST iteration computes no S(it+1); it loads the next item's Q and
+  // first K tiles instead (both K buffers and qreg are free by then).
   auto body = [&](auto bconst, int it, f16x (&s_cur)[2], f16x (&s_nxt)[2], h8 (&p_cur)[4],
-                  const h8 (&p_prev)[4], bool with_pv) {
+                  const h8 (&p_prev)[4], bool with_pv, bool has_next, const WorkItem& next) {
     constexpr int B = decltype(bconst)::value;
+    const bool last = it == ntiles - 1;
     char* const kfree = B == 0 ? sK0 : sK1;
     char* const knext = B == 0 ? sK1 : sK0;
     char* const vfree = B == 0 ? sV0 : sV1;
     char* const vprev = B == 0 ? sV1 : sV0;
     const int kb = tiles.at(it) * kTileK;
     // Loads issued last iteration have landed and every wavefront is done with last
-    // iteration's reads of the buffers about to be refilled.
-    __builtin_amdgcn_s_waitcnt(0);
+    // iteration's reads of the buffers about to be refilled.  Iteration 0 issued nothing since
+    // the item's start; only the previous item's O stores may still be in flight then.
+    if (with_pv)
+      __builtin_amdgcn_s_waitcnt(0);  // (gfx9 encoding 0: vmcnt/expcnt/lgkmcnt all zero)
+    else
+      wait_vmcnt<kStoreOps>();
     __syncthreads();
-    if (it + 2 < ntiles) load_tile(kfree, kbase, kstride_b, koff, tiles.at(it + 2));
-    load_tile(vfree, vbase, vstride_b, voff, tiles.at(it));
+    if (it + 2 < ntiles) load_tile(kfree, kbase, kstride_b, koff, tiles.at(it + 2), S);
+    load_tile(vfree, vbase, vstride_b, voff, tiles.at(it), S);
+    // The slot's last item re-loads its own Q / K(0) / K(1) as the "next" item (valid
+    // addresses, never used), so every path issues the same vector-memory instruction count and
+    // the waits below stay exact.
+    if (last) start_loads(next);
     if (!tile_full(kb, wq0, wq1, S, mask)) apply_mask(s_cur, kb);
-    qk(knext, s_nxt);
+    if (!last) {
+      qk(knext, s_nxt);
+    } else {
+      // No S(it+1) on the last tile.  Defining the set anyway (cheaply) keeps its previous
+      // contents from staying live across the softmax.
+      s_nxt[0] = f16x{};
+      s_nxt[1] = f16x{};
+    }
     if (with_pv) pv(vprev, p_prev);
     float alpha;
     const bool need = softmax(s_cur, p_cur, alpha);
@@ -287,37 +369,92 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     // compiler sinks the exponentials below the rescale branch, where no MFMA work overlaps them.
     asm volatile("" ::"v"(p_cur[0]), "v"(p_cur[1]), "v"(p_cur[2]), "v"(p_cur[3]), "v"(l_run));
     rescale(need, alpha);
+    if (last) {
+      // The item's last PV.  V(it) has landed once at most the next item's kPrefetchOps loads
+      // are in flight.  (Here, not after the loop, so the V buffer stays a compile-time choice
+      // and the compiler's own LDS-DMA wait can count the same way.)
+      wait_vmcnt<kPrefetchOps>();
+      __syncthreads();
+      pv(vfree, p_cur);
+    }
   };
 
-  body(std::integral_constant<int, 0>{}, 0, sA, sB, pA, pB, false);
-  for (int it = 1; it < ntiles; it += 2) {
-    body(std::integral_constant<int, 1>{}, it, sB, sA, pB, pA, true);
-    if (it + 1 < ntiles) body(std::integral_constant<int, 0>{}, it + 1, sA, sB, pA, pB, true);
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if ((ntiles - 1) & 1)
-    pv(sV1, pB);
-  else
-    pv(sV0, pA);
-
-  // ---- epilogue: O = O^T / l, lane owns row q_pos, dims 32db + 8g + 4hl + 0..3 ----
-  const float l_tot = pair_sum(l_run);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  if (q_pos < S) {
-    half_t* orow = p.o + (int64_t)(seq_start + q_pos) * p.o_stride + head * kHeadDim;
-    half_t* lrow = (p.o_last && q_pos == S - 1) ? p.o_last + (int64_t)seq * (kQHeads * kHeadDim) + head * kHeadDim : nullptr;
+  // The item's last PV and its output rows.  O = O^T / l; lane pair (l, l^32) holds row q_pos,
+  // dims 32db + 8g + 4hl + 0..3; one permlane32 swap per dword leaves each lane 8 consecutive
+  // dims (16 B): g = 2gp in the low half-wave, g = 2gp+1 in the high one.
+  auto epilogue = [&]() {
+    const float l_tot = pair_sum(l_run);
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    const int head = kvh * kGroup + head_in_group;
+    const auto ors = make_rsrc(p.o + (int64_t)seq_start * p.o_stride + head * kHeadDim, (uint32_t)S * ostride_b);
+    const auto lrs = make_rsrc(p.o_last + (int64_t)seq * (kQHeads * kHeadDim) + head * kHeadDim,
+                               p.o_last ? kRowBytes : 0u);
+    // Rows past the sequence (and every row but the last, for o_last) get an offset beyond the
+    // resource, so their stores are dropped; S * ostride_b < 2^31 is validated on the host.
+    const uint32_t orow = (q_pos < S ? (uint32_t)q_pos * ostride_b : 0x80000000u) + 16u * hl;
+    const uint32_t lrow = (q_pos == S - 1 ? 0u : 0x80000000u) + 16u * hl;
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const h4 val = {(half_t)(o[db][4 * g + 0] * inv), (half_t)(o[db][4 * g + 1] * inv),
-                        (half_t)(o[db][4 * g + 2] * inv), (half_t)(o[db][4 * g + 3] * inv)};
-        const int d = 32 * db + 8 * g + 4 * hl;
-        *reinterpret_cast<h4*>(orow + d) = val;
-        if (lrow) *reinterpret_cast<h4*>(lrow + d) = val;
+      for (int gp = 0; gp < 2; ++gp) {
+        const f16x& v = o[db];
+        const int ga = 4 * (2 * gp), gb = 4 * (2 * gp + 1);
+        const uint32_t a0 = pack2(v[ga] * inv, v[ga + 1] * inv), a1 = pack2(v[ga + 2] * inv, v[ga + 3] * inv);
+        const uint32_t b0 = pack2(v[gb] * inv, v[gb + 1] * inv), b1 = pack2(v[gb + 2] * inv, v[gb + 3] * inv);
+        const auto r0 = __builtin_amdgcn_permlane32_swap(a0, b0, false, false);
+        const auto r1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
+        const u4 val = {r0[0], r1[0], r0[1], r1[1]};
+        const uint32_t d = 2u * (32 * db + 16 * gp);  // + 16 hl, already in orow / lrow
+        __builtin_amdgcn_raw_buffer_store_b128(val, lrs, lrow + d, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(val, ors, orow + d, 0, 0);
       }
+  };
+
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+
+  WorkItem cur = work(i_begin);
+  start_loads(cur);
+  __builtin_amdgcn_s_waitcnt(0);
+  for (int wi = i_begin; wi < i_end; ++wi) {
+    const bool has_next = wi + 1 < i_end;
+    const WorkItem next = work(has_next ? wi + 1 : wi);
+    seq_start = cur.seq_start;
+    S = cur.seq_len;
+    kvh = cur.seq_kvh & 15;
+    seq = cur.seq_kvh >> 4;
+    const int blk_q0 = cur.q_block * kBlockQ;
+    wq0 = blk_q0 + wave_q;
+    wq1 = min(S - 1, wq0 + kWaveQ - 1);
+    q_pos = wq0 + lq;
+    ps = min(S, mask.prefix);
+    ws = min(S, mask.window);
+    tiles = key_tiles(blk_q0, min(S, blk_q0 + kBlockQ) - 1, S, mask);
+    ntiles = tiles.count();
+    kbase = reinterpret_cast<const char*>(p.k + (int64_t)seq_start * p.k_stride + kvh * kHeadDim);
+    vbase = reinterpret_cast<const char*>(p.v + (int64_t)seq_start * p.v_stride + kvh * kHeadDim);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) o[db] = f16x{};
+    m_run = -INFINITY;
+    l_run = 0.f;
+
+    // Q, K(0), K(1) of this item have landed: all but the previous item's O stores (the newest
+    // kStoreOps operations; the first item's loads were waited for above).
+    wait_vmcnt<kStoreOps>();
+    __syncthreads();
+    qk(sK0, sA);
+
+    body(I0{}, 0, sA, sB, pA, pB, false, has_next, next);
+    for (int it = 1; it < ntiles; it += 2) {
+      body(I1{}, it, sB, sA, pB, pA, true, has_next, next);
+      if (it + 1 < ntiles) body(I0{}, it + 1, sA, sB, pA, pB, true, has_next, next);
+    }
+    epilogue();
+    cur = next;
   }
+  // The last item's unused prefetch (LDS-DMA included) lands before the workgroup leaves.
+  __builtin_amdgcn_s_waitcnt(0);
 }
 
 // Retained-key bitmask of one sequence through the kernel's own key iteration (kept_keys_row):
@@ -329,8 +466,8 @@ __global__ void debug_mask_kernel(int S, MaskSpec mask, uint32_t* bits, int word
 }
 
 hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream) {
-  if (p.n_work <= 0) return hipSuccess;
-  hipLaunchKernelGGL(attn_fwd_kernel, dim3(p.n_work), dim3(kThreads), 0, stream, p);
+  if (p.n_slots <= 0) return hipSuccess;
+  hipLaunchKernelGGL(attn_fwd_kernel, dim3(p.n_slots), dim3(kThreads), 0, stream, p);
   return hipGetLastError();
 }
 

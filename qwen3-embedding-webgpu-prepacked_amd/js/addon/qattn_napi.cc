@@ -364,6 +364,7 @@ napi_value info_object(napi_env env, const qattn_run_info& i) {
   set("workItems", i.work_items);
   set("blockQueries", i.block_queries);
   set("tilePairs", (double)i.tile_pairs);
+  set("slots", i.slots);
   return out;
 }
 

@@ -48,7 +48,7 @@ export class DeviceContext {
 
 export interface RunInfo {
   tokens: number; pairs: number; flops: number; bytes: number;
-  workItems: number; blockQueries: number; tilePairs: number;
+  workItems: number; blockQueries: number; tilePairs: number; slots: number;
 }
 export interface AttentionRun { handle: unknown; info: RunInfo; cuSeqlens: Int32Array }
 export interface VarlenOptions {

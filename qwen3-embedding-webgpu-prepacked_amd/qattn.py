@@ -45,6 +45,7 @@ class RunInfo(ctypes.Structure):
         ("tokens", ctypes.c_int64), ("pairs", ctypes.c_int64), ("flops", ctypes.c_int64),
         ("bytes", ctypes.c_int64), ("work_items", ctypes.c_int32),
         ("block_queries", ctypes.c_int32), ("tile_pairs", ctypes.c_int64),
+        ("slots", ctypes.c_int32), ("reserved", ctypes.c_int32),
     ]
 
     def as_dict(self):
@@ -88,6 +89,7 @@ def lib():
         "qattn_run_get_info": (ctypes.c_int, [vp, ctypes.POINTER(RunInfo)]),
         "qattn_plan_describe": (ctypes.c_int, [ctypes.POINTER(RunDesc), vp, i32,
                                                ctypes.POINTER(i32), ctypes.POINTER(RunInfo)]),
+        "qattn_plan_slots": (ctypes.c_int, [ctypes.POINTER(RunDesc), i32, vp, i32, ctypes.POINTER(i32)]),
         "qattn_prefill": (ctypes.c_int, [vp, ctypes.POINTER(RunDesc), vp]),
         "qattn_debug_mask": (ctypes.c_int, [vp, i32, i32, i32, i32, vp]),
         "qattn_plan_mask": (ctypes.c_int, [i32, i32, i32, i32, vp]),
@@ -132,8 +134,17 @@ def make_desc(q, k, v, o, cu_seqlens, mask=MASK_PREFIX_LOCAL, prefix=176, window
     return d
 
 
+def plan_slots(desc, max_slots=0):
+    """Host-only planner: slot offsets int32[nslots+1] into plan_describe's item list."""
+    n = ctypes.c_int32(0)
+    _check(lib().qattn_plan_slots(ctypes.byref(desc), max_slots, None, 0, ctypes.byref(n)))
+    out = np.zeros(n.value + 1, dtype=np.int32)
+    _check(lib().qattn_plan_slots(ctypes.byref(desc), max_slots, _np_ptr(out), n.value + 1, ctypes.byref(n)))
+    return out
+
+
 def plan_describe(desc):
-    """Host-only planner: (work items int32[n,4] in launch order, RunInfo)."""
+    """Host-only planner: (work items int32[n,4] grouped by slot, RunInfo)."""
     n = ctypes.c_int32(0)
     info = RunInfo()
     _check(lib().qattn_plan_describe(ctypes.byref(desc), None, 0, ctypes.byref(n), ctypes.byref(info)))

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol(qattn):
 
 
 def test_abi_version(qattn):
-    assert qattn.lib().qattn_abi_version() == 1
+    assert qattn.lib().qattn_abi_version() == 2
 
 
 def test_create_without_gpu_fails_cleanly(qattn):
@@ -45,17 +45,37 @@ def test_create_without_gpu_fails_cleanly(qattn):
 
 
 @pytest.mark.parametrize("lengths,mask", [([50], 1), ([500] * 16, 1), ([5000], 1), ([1500], 1),
-                                          ([10, 150, 64, 65, 1], 0), ([5000] * 4, 1)])
-def test_planner_covers_every_block_once_heaviest_first(qattn, oracle, lengths, mask):
-    items, info = qattn.plan_describe(_desc(qattn, lengths, mask))
+                                          ([10, 150, 64, 65, 1], 0), ([5000] * 4, 1), ([500] * 16, 0)])
+def test_planner_covers_every_block_once_in_balanced_slots(qattn, oracle, lengths, mask):
+    d = _desc(qattn, lengths, mask)
+    items, info = qattn.plan_describe(d)
+    slots = qattn.plan_slots(d)
     want = {(int(np.sum(lengths[:s])), L, qb, (s << 4) | g)
             for s, L in enumerate(lengths) for qb in range((L + 63) // 64) for g in range(8)}
     got = [tuple(int(x) for x in it) for it in items]
     assert len(got) == len(want) == info.work_items
     assert set(got) == want
-    # heaviest first: the number of key tiles visited never increases along the list
-    ntiles = [len(_tiles(it[2], it[1], mask)) for it in got]
-    assert all(a >= b for a, b in zip(ntiles, ntiles[1:]))
+    # slot structure: offsets cover the list; slot b holds only KV heads g with g % 8 == b % 8
+    # (workgroup b runs on XCD b % 8), heaviest first; at most 512 slots (256 CUs x 2)
+    assert slots[0] == 0 and slots[-1] == len(got) and np.all(np.diff(slots) >= 0)
+    assert info.slots == len(slots) - 1 <= 512
+    cost = lambda it: 4 * len(_tiles(it[2], it[1], mask)) + 3
+    loads = np.zeros(len(slots) - 1, dtype=np.int64)
+    for b in range(len(slots) - 1):
+        mine = got[slots[b]:slots[b + 1]]
+        assert all((it[3] & 15) % 8 == b % 8 for it in mine)
+        c = [cost(it) for it in mine]
+        assert c == sorted(c, reverse=True)
+        loads[b] = sum(c)
+    # longest-processing-time bound per XCD group: no slot exceeds the group's mean load by
+    # more than one item
+    for g in range(8):
+        grp = [it for it in got if (it[3] & 15) % 8 == g]
+        if not grp:
+            continue
+        used = loads[g::8][loads[g::8] > 0]
+        mean = sum(cost(it) for it in grp) / len(used)
+        assert used.max() <= mean + max(cost(it) for it in grp)
     # figures
     pairs = sum(oracle.mask_pairs(L, mask) for L in lengths)
     assert info.tokens == sum(lengths)
@@ -63,6 +83,14 @@ def test_planner_covers_every_block_once_heaviest_first(qattn, oracle, lengths, 
     assert info.flops == 8192 * pairs
     assert info.bytes == 12288 * sum(lengths)
     assert info.tile_pairs >= pairs
+
+
+def test_planner_slot_count_follows_the_limit(qattn):
+    d = _desc(qattn, [500] * 16, 1)
+    assert len(qattn.plan_slots(d, 64)) - 1 == 64
+    assert len(qattn.plan_slots(d, 8)) - 1 == 8
+    small = _desc(qattn, [50], 1)  # 8 items: one per KV head, one slot each
+    assert len(qattn.plan_slots(small)) - 1 == 8
 
 
 def _tiles(qb, L, mask, P=176, W=432):
