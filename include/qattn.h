@@ -103,11 +103,24 @@ typedef struct qattn_run_desc {
   /* Optional fp16 [nseq][16*128] device output: row i receives O of token cu_seqlens[i+1]-1,
    * the row the reference's last-token pool reads (ops.ts:357).  NULL to skip. */
   void* o_last;
+  /* enum qattn_run_flags (0: defaults). */
+  int32_t flags;
 } qattn_run_desc;
+
+enum qattn_run_flags {
+  /* Never split an item's key tiles across workgroups (split-K).  Every output row is then
+   * computed by one pass in a fixed order, so a sequence gives bitwise the same result alone or
+   * in any batch, as the reference does; without the flag the planner may split long items to
+   * balance the GPU, and results stay deterministic for a given batch but may differ from another
+   * batch's in the last fp16 bit. */
+  QATTN_FLAG_BATCH_INVARIANT = 1
+};
 
 /* Plans the launch (validates, builds the work list of (sequence, kv_head, query block) items,
  * spreads it over persistent workgroups -- "slots", two per compute unit -- longest first with
- * each KV head's items on one XCD, uploads it) and returns a run that owns its device work list. */
+ * each KV head's items on one XCD, splitting long items' key tiles over several slots unless
+ * QATTN_FLAG_BATCH_INVARIANT, uploads it) and returns a run that owns its device work list and
+ * split-K workspace. */
 int qattn_run_create(qattn_ctx* ctx, const qattn_run_desc* desc, qattn_run** out);
 /* Enqueues the attention kernel of a run on `stream` (NULL: the context stream). */
 int qattn_run_encode(qattn_run* run, qattn_stream_t stream);
@@ -124,22 +137,26 @@ typedef struct qattn_run_info {
   int32_t work_items;       /* (sequence, kv_head, 64-query block) items */
   int32_t block_queries;    /* query positions per work item */
   int64_t tile_pairs;       /* (query, key) pairs inside the MFMA tiles computed, per query head */
-  int32_t slots;            /* persistent workgroups launched (each runs a list of items) */
-  int32_t reserved;
+  int32_t slots;            /* persistent workgroups launched (each runs a list of entries) */
+  int32_t split_items;      /* items whose key tiles are spread over several entries (split-K) */
 } qattn_run_info;
 int qattn_run_get_info(const qattn_run* run, qattn_run_info* info);
 
 /* Host-only planning (no device needed): validates `desc` exactly as qattn_run_create does and
- * reports the work list a run on an MI355X (256 compute units, 512 slots) would upload: items
- * grouped by slot, heaviest first within a slot.  Each item is four int32:
- * {first token of the sequence, sequence length, query block, sequence<<4 | kv_head}.
- * `items` may be NULL (count only); `*count` receives the number of items, `info` (optional) the
- * run's figures.  Fails with QATTN_EINVAL if `capacity` is too small for a non-NULL `items`.
+ * reports the work list a run on an MI355X (256 compute units, 512 slots) would upload: entries
+ * grouped by slot, heaviest first within a slot.  Each entry is eight int32:
+ * {first token of the sequence, sequence length, query block, sequence<<4 | kv_head,
+ *  first key tile, end key tile (indices into the item's visited key tiles), split, part}.
+ * An item spread over several entries (chunks, split-K) has split >= 0 (shared by its chunks) and
+ * part = chunk index | chunk count << 4 | first partial-result index << 8; otherwise split = -1,
+ * part = 0 and the entry covers all of the item's tiles.  `items` may be NULL (count only);
+ * `*count` receives the number of entries, `info` (optional) the run's figures.  Fails with
+ * QATTN_EINVAL if `capacity` (entries) is too small for a non-NULL `items`.
  * Replaces the reference's dispatch-size computation (ops.ts:329-343). */
 int qattn_plan_describe(const qattn_run_desc* desc, int32_t* items, int32_t capacity,
                         int32_t* count, qattn_run_info* info);
 /* The slot structure of the same plan for at most `max_slots` workgroups (<= 0: 512): slot b
- * runs items slot_begin[b] .. slot_begin[b+1]-1 of qattn_plan_describe's list and is dispatched
+ * runs entries slot_begin[b] .. slot_begin[b+1]-1 of qattn_plan_describe's list and is dispatched
  * to XCD b % 8.  `*nslots` receives the slot count; `slot_begin` (optional, `capacity` >=
  * nslots + 1 entries) the offsets. */
 int qattn_plan_slots(const qattn_run_desc* desc, int32_t max_slots, int32_t* slot_begin,
@@ -149,6 +166,13 @@ int qattn_plan_slots(const qattn_run_desc* desc, int32_t max_slots, int32_t* slo
 int qattn_prefill(qattn_ctx* ctx, const qattn_run_desc* desc, qattn_stream_t stream);
 
 /* ---- mask check  (same device predicate and key-tile iterator as the attention kernel) ---- */
+/* Diagnostic, no counterpart in the reference: the XCD (hardware XCC_ID) that each of n
+ * workgroups of a launch shaped like the attention kernel's runs on.  The planner keeps each KV
+ * head's work on slots b with one value of b % 8, expecting round-robin dispatch (workgroup b on
+ * XCD b % number-of-XCDs) to keep that head's K/V in one L2; this makes the expectation testable.
+ * (Only locality depends on it, not results.) */
+int qattn_debug_xcd_map(qattn_ctx* ctx, int32_t n, int32_t* host_out);
+
 /* Writes the retained-key bitmask of one sequence of length L to host memory: word
  * q*ceil(L/32) + k/32, bit k%32 set iff the attention kernel visits key k for query q and keeps
  * it.  Must equal the reference predicate ops.ts:205-209,219-220 bit for bit. */

@@ -31,16 +31,21 @@ struct AttnParams {
   const half_t* v;
   half_t* o;
   half_t* o_last;
-  int64_t q_stride, k_stride, v_stride, o_stride;
+  uint32_t q_stride_b, k_stride_b, v_stride_b, o_stride_b;
   const WorkItem* work;
   const int32_t* slot_begin;
   int32_t n_slots;
   MaskSpec mask;
   float scale_log2;
+  float* partials;          // split chunks' partial results (kPartialBytes each)
+  const WorkItem* splits;   // chunk 0 of each split item
+  int32_t n_splits;
 };
 hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream);
+hipError_t launch_attn_merge(const AttnParams& p, hipStream_t stream);
 hipError_t launch_debug_mask(int S, MaskSpec mask, uint32_t* bits, int words_per_row,
                              hipStream_t stream);
+hipError_t launch_xcd_map(int* out, int n, hipStream_t stream);
 hipError_t launch_fill_normal(half_t* dst, int64_t rows, int64_t row_elems, int64_t row_stride,
                               uint64_t seed, hipStream_t stream);
 hipError_t launch_fill_token_rows(half_t* dst, const int32_t* ids, int64_t rows, int64_t row_elems,
@@ -65,6 +70,7 @@ struct qattn_run {
   qattn_ctx* ctx = nullptr;
   AttnParams params{};
   void* plan_dev = nullptr;  // work items by slot, then the slot offsets
+  void* split_dev = nullptr; // the chunks' partial results (merged by a second kernel)
   int64_t v_offset = 0;
   bool has_o_last = false;
   qattn_run_info info{};
@@ -141,6 +147,7 @@ int validate_desc(qattn_ctx* ctx, const qattn_run_desc* d) {
   if ((d->q_row_stride | d->k_row_stride | d->v_row_stride | d->o_row_stride | d->v_offset) & 7)
     return fail(ctx, QATTN_EINVAL, "row strides and v_offset must be multiples of 8 elements");
   if (d->v_offset < 0) return fail(ctx, QATTN_EINVAL, "v_offset must be >= 0");
+  if (d->flags & ~QATTN_FLAG_BATCH_INVARIANT) return fail(ctx, QATTN_EINVAL, "unknown flags 0x%x", d->flags);
   if (d->mask != QATTN_MASK_CAUSAL && d->mask != QATTN_MASK_PREFIX_LOCAL)
     return fail(ctx, QATTN_EINVAL, "unknown mask kind %d", d->mask);
   if (d->mask == QATTN_MASK_PREFIX_LOCAL) {
@@ -312,17 +319,27 @@ namespace {
 constexpr int kXcds = 8;
 constexpr int kBlocksPerCU = 2;
 constexpr int kDefaultSlots = 256 * kBlocksPerCU;  // MI355X: 256 CUs
+// Partial result of one chunk: per wavefront (4) and lane (64), the 64 fp32 O^T accumulators
+// of the lane's row, then m and l (log2-domain row max, row sum) and two pad words.
+constexpr int kPartialFloats = 68;
+constexpr size_t kPartialBytes = (size_t)kWaves * 64 * kPartialFloats * 4;
 
 struct Plan {
   std::vector<WorkItem> items;       // grouped by slot, heaviest first within a slot
   std::vector<int32_t> slot_begin;   // n_slots + 1 offsets into items
+  std::vector<WorkItem> split_heads; // chunk 0 of each split item, by split id
+  int32_t splits = 0;                // items spread over several chunks
+  int32_t partials = 0;              // chunk partial-result records the workspace holds
 };
 
-// Relative cost of a work item for load balancing: its key tiles plus a fixed share for the
-// item's start (Q and first tiles) and end (last PV, O stores) that the pipeline cannot hide.
+// Relative cost of a piece of work for load balancing, in quarter tiles: its key tiles plus a
+// fixed share for its start (Q and first tiles) and end (last PV, O stores) that the pipeline
+// cannot hide; a chunk of a split item also writes / merges a partial result.
 int item_cost(int ntiles) { return 4 * ntiles + 3; }
+constexpr int kChunkExtra = 4;
+constexpr int kMinChunkTiles = 2;
 
-// The planner: validated description -> work items grouped into slots + run figures.
+// The planner: validated description -> work entries grouped into slots + run figures.
 int plan_work(qattn_ctx* ctx, const qattn_run_desc* d, int max_slots, Plan* out,
               qattn_run_info* info_out, MaskSpec* mask_out) {
   int rc = validate_desc(ctx, d);
@@ -332,7 +349,7 @@ int plan_work(qattn_ctx* ctx, const qattn_run_desc* d, int max_slots, Plan* out,
                       d->mask == QATTN_MASK_PREFIX_LOCAL ? d->window : 0};
   struct Item {
     WorkItem w;
-    int cost;
+    int ntiles;
   };
   std::vector<Item> group_items[kXcds];
   qattn_run_info info{};
@@ -349,24 +366,111 @@ int plan_work(qattn_ctx* ctx, const qattn_run_desc* d, int max_slots, Plan* out,
       // [q0+32, q0+63] each compute every tile of the work item.
       info.tile_pairs += (int64_t)tr.count() * (q0 + kWaveQ < L ? 2 : 1) * kWaveQ * kTileK;
       for (int g = 0; g < kKVHeads; ++g)
-        group_items[g % kXcds].push_back({WorkItem{start, L, qb, (s << 4) | g}, item_cost(tr.count())});
+        group_items[g % kXcds].push_back({WorkItem{start, L, qb, (s << 4) | g, 0, tr.count(), -1, 0}, tr.count()});
+      ++info.work_items;
     }
   }
-  // Longest processing time first, per XCD group: items in falling cost (stable, so equal items
-  // keep sequence order) each go to the least loaded of the group's slots.
+  info.work_items *= kKVHeads;
+  // Per XCD group, longest processing time first with split-K: items in falling cost (stable,
+  // so equal items keep sequence order) each go whole to the least loaded slot if that keeps it
+  // within a target makespan T; otherwise the item is cut into chunks of key tiles that fill the
+  // least loaded slots up to T (the chunks' partial softmax states are merged by a second
+  // kernel).  T is scanned upward from the mean load; the plan with the smallest
+  // makespan (then fewest chunks) wins.
   const int per_group = max_slots / kXcds;
-  std::vector<std::vector<int>> lists[kXcds];
+  const bool may_split = !(d->flags & QATTN_FLAG_BATCH_INVARIANT);
+  std::vector<std::vector<WorkItem>> lists[kXcds];
   int used = 0;
   for (int g = 0; g < kXcds; ++g) {
     auto& items = group_items[g];
-    std::stable_sort(items.begin(), items.end(), [](const Item& a, const Item& b) { return a.cost > b.cost; });
+    std::stable_sort(items.begin(), items.end(), [](const Item& a, const Item& b) { return a.ntiles > b.ntiles; });
     const int m = std::min<int>(per_group, (int)items.size());
+    if (!m) continue;
+    int64_t total = 0;
+    int max_tiles = 0;
+    for (const Item& it : items) {
+      total += item_cost(it.ntiles);
+      max_tiles = std::max(max_tiles, it.ntiles);
+    }
+    // One greedy pass for target T: per item, (slot, tile range) pieces; returns the makespan.
+    struct Piece {
+      int slot, item, a, b;
+    };
+    auto greedy = [&](int64_t T, std::vector<Piece>* pieces, int* nchunks) {
+      std::vector<int64_t> load(m, 0);
+      // min-heap of (load, slot)
+      std::vector<std::pair<int64_t, int>> heap;
+      for (int j = 0; j < m; ++j) heap.push_back({0, j});
+      auto cmp = [](const std::pair<int64_t, int>& x, const std::pair<int64_t, int>& y) { return x > y; };
+      std::make_heap(heap.begin(), heap.end(), cmp);
+      auto pop = [&]() { std::pop_heap(heap.begin(), heap.end(), cmp); auto t = heap.back(); heap.pop_back(); return t.second; };
+      auto push = [&](int j) { heap.push_back({load[j], j}); std::push_heap(heap.begin(), heap.end(), cmp); };
+      pieces->clear();
+      *nchunks = 0;
+      for (int i = 0; i < (int)items.size(); ++i) {
+        const int n = items[i].ntiles;
+        int j = pop();
+        if (load[j] + item_cost(n) <= T || n < 2 * kMinChunkTiles || !may_split) {
+          load[j] += item_cost(n);
+          pieces->push_back({j, i, 0, n});
+          push(j);
+          continue;
+        }
+        std::vector<Piece> mine;
+        int a = 0;
+        while (a < n) {
+          if (!mine.empty()) j = pop();
+          const int rest = n - a;
+          // Room left under T on the least loaded slot; none: the rest goes there whole.
+          int take = (int)((T - load[j] - 3 - kChunkExtra) / 4);
+          if (take < kMinChunkTiles || (int)mine.size() == kMaxChunks - 1 || take >= rest ||
+              rest - take < kMinChunkTiles)
+            take = rest;
+          mine.push_back({j, i, a, a + take});
+          load[j] += item_cost(take) + kChunkExtra;
+          push(j);
+          a += take;
+        }
+        if (mine.size() == 1) load[mine[0].slot] -= kChunkExtra;  // not split after all
+        else *nchunks += (int)mine.size();
+        pieces->insert(pieces->end(), mine.begin(), mine.end());
+      }
+      return *std::max_element(load.begin(), load.end());
+    };
+    std::vector<Piece> best, trial;
+    int64_t best_span = -1;
+    int best_chunks = 0;
+    const int64_t lo = (total + m - 1) / m;
+    for (int64_t T = lo; T <= lo + 4 * max_tiles + 8; ++T) {
+      int nch = 0;
+      const int64_t span = greedy(T, &trial, &nch);
+      if (best_span < 0 || span < best_span || (span == best_span && nch < best_chunks)) {
+        best_span = span;
+        best_chunks = nch;
+        best.swap(trial);
+      }
+      if (best_span <= lo || !may_split) break;
+    }
+    // Emit: per slot in assignment order; chunks of one item share a split id and partials.
     lists[g].assign(m, {});
-    std::vector<int64_t> load(m, 0);
-    for (int i = 0; i < (int)items.size(); ++i) {
-      const int j = (int)(std::min_element(load.begin(), load.end()) - load.begin());
-      lists[g][j].push_back(i);
-      load[j] += items[i].cost;
+    for (size_t k = 0; k < best.size();) {
+      size_t e = k + 1;
+      while (e < best.size() && best[e].item == best[k].item) ++e;
+      const WorkItem base = items[best[k].item].w;
+      const int nch = (int)(e - k);
+      const int split = nch > 1 ? out->splits++ : -1;
+      const int first = nch > 1 ? out->partials : 0;
+      if (nch > 1) out->partials += nch;
+      for (size_t c = k; c < e; ++c) {
+        WorkItem w = base;
+        w.tile_begin = best[c].a;
+        w.tile_end = best[c].b;
+        w.split = split;
+        w.part = nch > 1 ? (int)(c - k) | (nch << 4) | (first << 8) : 0;
+        if (nch > 1 && c == k) out->split_heads.push_back(w);
+        lists[g][best[c].slot].push_back(w);
+      }
+      k = e;
     }
     used = std::max(used, m);
   }
@@ -375,11 +479,11 @@ int plan_work(qattn_ctx* ctx, const qattn_run_desc* d, int max_slots, Plan* out,
   for (int j = 0; j < used; ++j)
     for (int g = 0; g < kXcds; ++g) {
       if (j < (int)lists[g].size())
-        for (int i : lists[g][j]) out->items.push_back(group_items[g][i].w);
+        for (const WorkItem& w : lists[g][j]) out->items.push_back(w);
       out->slot_begin.push_back((int32_t)out->items.size());
     }
-  info.work_items = (int32_t)out->items.size();
   info.slots = (int32_t)out->slot_begin.size() - 1;
+  info.split_items = out->splits;
   info.flops = 4ll * kHeadDim * kQHeads * info.pairs;
   info.bytes = 12288ll * info.tokens + (d->o_last ? 4096ll * d->nseq : 0);
   if (info_out) *info_out = info;
@@ -402,7 +506,8 @@ int qattn_plan_describe(const qattn_run_desc* desc, int32_t* items, int32_t capa
   if (info) *info = inf;
   if (items) {
     if (capacity < (int32_t)plan.items.size())
-      return fail(nullptr, QATTN_EINVAL, "capacity %d < %zu work items", capacity, plan.items.size());
+      return fail(nullptr, QATTN_EINVAL, "capacity %d < %zu work entries", capacity, plan.items.size());
+    static_assert(sizeof(WorkItem) == 8 * sizeof(int32_t), "work entry is 8 int32");
     std::memcpy(items, plan.items.data(), plan.items.size() * sizeof(WorkItem));
   }
   return QATTN_OK;
@@ -438,12 +543,15 @@ int qattn_run_create(qattn_ctx* ctx, const qattn_run_desc* d, qattn_run** out) {
   run->info = info;
   run->v_offset = d->v_offset;
   run->has_o_last = d->o_last != nullptr;
-  // One upload: the items, then the slot offsets (16-byte items keep the offsets aligned).
+  // One upload: the entries, the split items' chunk-0 entries, then the slot offsets (32-byte
+  // entries keep the offsets aligned).
   const size_t items_bytes = plan.items.size() * sizeof(WorkItem);
+  const size_t heads_bytes = plan.split_heads.size() * sizeof(WorkItem);
   const size_t slots_bytes = plan.slot_begin.size() * sizeof(int32_t);
-  std::vector<char> host(items_bytes + slots_bytes);
+  std::vector<char> host(items_bytes + heads_bytes + slots_bytes);
   if (items_bytes) std::memcpy(host.data(), plan.items.data(), items_bytes);
-  std::memcpy(host.data() + items_bytes, plan.slot_begin.data(), slots_bytes);
+  if (heads_bytes) std::memcpy(host.data() + items_bytes, plan.split_heads.data(), heads_bytes);
+  std::memcpy(host.data() + items_bytes + heads_bytes, plan.slot_begin.data(), slots_bytes);
   {
     DeviceGuard g(ctx->device);
     hipError_t e = hipMalloc(&run->plan_dev, host.size());
@@ -458,18 +566,33 @@ int qattn_run_create(qattn_ctx* ctx, const qattn_run_desc* d, qattn_run** out) {
       return fail(ctx, QATTN_EHIP, "hipMemcpy(work list): %s", hipGetErrorString(e));
     }
   }
+  // Split items: the chunks' partial results.
+  if (plan.splits) {
+    DeviceGuard g(ctx->device);
+    hipError_t e = hipMalloc(&run->split_dev, (size_t)plan.partials * kPartialBytes);
+    if (e != hipSuccess) {
+      if (run->split_dev) (void)hipFree(run->split_dev);
+      (void)hipFree(run->plan_dev);
+      delete run;
+      return fail(ctx, QATTN_ENOMEM, "split workspace (%d chunks): %s", plan.partials, hipGetErrorString(e));
+    }
+  }
   AttnParams& p = run->params;
+  p.partials = static_cast<float*>(run->split_dev);
+  p.splits = reinterpret_cast<const WorkItem*>(static_cast<const char*>(run->plan_dev) + items_bytes);
+  p.n_splits = plan.splits;
   p.q = static_cast<const half_t*>(d->q);
   p.k = static_cast<const half_t*>(d->k);
   p.v = static_cast<const half_t*>(d->v) + d->v_offset;
   p.o = static_cast<half_t*>(d->o);
   p.o_last = static_cast<half_t*>(d->o_last);
-  p.q_stride = d->q_row_stride;
-  p.k_stride = d->k_row_stride;
-  p.v_stride = d->v_row_stride;
-  p.o_stride = d->o_row_stride;
+  // Byte strides fit 32 bits: (L + 64) * stride * 2 < 2^31 is validated for every sequence.
+  p.q_stride_b = (uint32_t)(d->q_row_stride * 2);
+  p.k_stride_b = (uint32_t)(d->k_row_stride * 2);
+  p.v_stride_b = (uint32_t)(d->v_row_stride * 2);
+  p.o_stride_b = (uint32_t)(d->o_row_stride * 2);
   p.work = static_cast<const WorkItem*>(run->plan_dev);
-  p.slot_begin = reinterpret_cast<const int32_t*>(static_cast<const char*>(run->plan_dev) + items_bytes);
+  p.slot_begin = reinterpret_cast<const int32_t*>(static_cast<const char*>(run->plan_dev) + items_bytes + heads_bytes);
   p.n_slots = info.slots;
   p.mask = mask;
   p.scale_log2 = (float)(1.4426950408889634 / std::sqrt(128.0));
@@ -482,6 +605,7 @@ int qattn_run_encode(qattn_run* run, qattn_stream_t stream) {
   qattn_ctx* ctx = run->ctx;
   DeviceGuard g(ctx->device);
   HIP_TRY(ctx, launch_attn_fwd(run->params, pick_stream(ctx, stream)));
+  HIP_TRY(ctx, launch_attn_merge(run->params, pick_stream(ctx, stream)));
   return QATTN_OK;
 }
 
@@ -504,10 +628,11 @@ int qattn_run_rebind(qattn_run* run, const void* q, const void* k, const void* v
 
 void qattn_run_destroy(qattn_run* run) {
   if (!run) return;
-  if (run->plan_dev) {
+  if (run->plan_dev || run->split_dev) {
     DeviceGuard g(run->ctx->device);
     (void)hipStreamSynchronize(run->ctx->stream);
-    (void)hipFree(run->plan_dev);
+    if (run->plan_dev) (void)hipFree(run->plan_dev);
+    if (run->split_dev) (void)hipFree(run->split_dev);
   }
   delete run;
 }
@@ -533,6 +658,19 @@ int qattn_prefill(qattn_ctx* ctx, const qattn_run_desc* desc, qattn_stream_t str
 }
 
 // ---- mask check -------------------------------------------------------------------------------
+
+int qattn_debug_xcd_map(qattn_ctx* ctx, int32_t n, int32_t* host_out) {
+  if (!ctx || !host_out || n <= 0 || n > (1 << 20)) return fail(ctx, QATTN_EINVAL, "bad arguments");
+  DeviceGuard g(ctx->device);
+  int* dev = nullptr;
+  HIP_TRY(ctx, hipMalloc(&dev, (size_t)n * sizeof(int)));
+  hipError_t e = launch_xcd_map(dev, n, ctx->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(host_out, dev, (size_t)n * sizeof(int), hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  (void)hipFree(dev);
+  if (e != hipSuccess) return fail(ctx, QATTN_EHIP, "xcd map: %s", hipGetErrorString(e));
+  return QATTN_OK;
+}
 
 int qattn_debug_mask(qattn_ctx* ctx, int32_t L, int32_t mask, int32_t prefix, int32_t window,
                      uint32_t* host_bits) {

@@ -114,12 +114,21 @@ __host__ __device__ inline void kept_keys_row(int q, int S, const MaskSpec& m, u
   }
 }
 
-// Work item of one launch: (sequence start token, length, query block, sequence<<4 | kv_head).
+// One work entry of a launch: key tiles [tile_begin, tile_end) of the key_tiles() list of the
+// item (sequence start token, length, query block, sequence<<4 | kv_head).  An item whose tiles
+// are spread over several entries ("chunks") has split >= 0: its chunks share counter `split`,
+// and part = ci | nchunks << 4 | first_partial << 8 (chunk ci of nchunks, whose partial
+// results sit at workspace index first_partial + ci).  Unsplit items have split = -1, part = 0.
 struct WorkItem {
   int seq_start;
   int seq_len;
   int q_block;
   int seq_kvh;
+  int tile_begin;
+  int tile_end;
+  int split;
+  int part;
 };
+constexpr int kMaxChunks = 15;  // nchunks fits 4 bits
 
 }  // namespace qattn

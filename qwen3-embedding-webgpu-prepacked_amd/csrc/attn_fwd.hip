@@ -53,13 +53,21 @@ struct AttnParams {
   const half_t* v;  // already offset by v_offset
   half_t* o;
   half_t* o_last;
-  int64_t q_stride, k_stride, v_stride, o_stride;
+  uint32_t q_stride_b, k_stride_b, v_stride_b, o_stride_b;  // row strides in bytes (< 2^31)
   const WorkItem* work;       // work items grouped by slot
   const int32_t* slot_begin;  // slot b owns work[slot_begin[b] .. slot_begin[b+1])
   int32_t n_slots;            // workgroups launched
   MaskSpec mask;
   float scale_log2;  // (1/sqrt(128)) * log2(e)
+  float* partials;          // split chunks' partial results (kPartialRecords x 64 lanes x 4 waves each)
+  const WorkItem* splits;   // chunk 0 of each split item, for the merge kernel
+  int32_t n_splits;
 };
+
+// Partial result of one chunk of a split item, per wavefront: 17 records of 64 lanes x float4
+// (records 0..15: the lane's 64 O^T accumulators, 16: m, l, 0, 0), so every access is a
+// coalesced 1 KiB row.
+constexpr int kPartialRecords = 17;
 
 // Vector-memory instructions per lane that one item's prologue loads (Q: 8 x 16 B, K tiles 0
 // and 1: kLoadsPerTile each) and that one item's epilogue stores (o_last row and O rows, 8 x 16 B
@@ -103,6 +111,49 @@ __device__ inline uint32_t pack2(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// Record 0 of partial result `index` for (wave, lane); record r is 64 float4 further per r.
+__device__ inline float __attribute__((ext_vector_type(4)))* partial_records(float* partials, int index,
+                                                                               int wave, int lane) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  return reinterpret_cast<f4*>(partials) + ((size_t)index * kWaves + wave) * kPartialRecords * 64 + lane;
+}
+
+// Output rows of one wavefront: O = O^T / l for query row q_pos (lanes l and l^32 share it,
+// dims 32db + 8g + 4hl + 0..3), fp16, into O and (for the sequence's last row) o_last.  One
+// permlane32 swap per dword leaves each lane 8 consecutive dims (16 B): g = 2gp in the low
+// half-wave, g = 2gp+1 in the high one.  Exactly kStoreOps buffer stores per lane; rows past the
+// sequence (and every row but the last, for o_last) get an offset beyond the buffer resource, so
+// their stores are dropped (S * o stride < 2^31 is validated on the host).
+__device__ inline void store_rows(const AttnParams& p, const f16x (&o)[4], float l_run, int seq_start,
+                                  int S, int seq, int head, int q_pos, int hl) {
+  const uint32_t ostride_b = p.o_stride_b;
+  const float l_tot = pair_sum(l_run);
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  const auto ors = make_rsrc(reinterpret_cast<const char*>(p.o) + (uint64_t)seq_start * ostride_b + head * kRowBytes,
+                             (uint32_t)S * ostride_b);
+  const auto lrs = make_rsrc(p.o_last + (int64_t)seq * (kQHeads * kHeadDim) + head * kHeadDim,
+                             p.o_last ? kRowBytes : 0u);
+  const uint32_t orow = (q_pos < S ? (uint32_t)q_pos * ostride_b : 0x80000000u) + 16u * hl;
+  const uint32_t lrow = (q_pos == S - 1 ? 0u : 0x80000000u) + 16u * hl;
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int gp = 0; gp < 2; ++gp) {
+      const f16x& v = o[db];
+      const int ga = 4 * (2 * gp), gb = 4 * (2 * gp + 1);
+      const uint32_t a0 = pack2(v[ga] * inv, v[ga + 1] * inv), a1 = pack2(v[ga + 2] * inv, v[ga + 3] * inv);
+      const uint32_t b0 = pack2(v[gb] * inv, v[gb + 1] * inv), b1 = pack2(v[gb + 2] * inv, v[gb + 3] * inv);
+      const auto r0 = __builtin_amdgcn_permlane32_swap(a0, b0, false, false);
+      const auto r1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
+      const u4 val = {r0[0], r1[0], r0[1], r1[1]};
+      const uint32_t d = 2u * (32 * db + 16 * gp);  // + 16 hl, already in orow / lrow
+      __builtin_amdgcn_raw_buffer_store_b128(val, lrs, lrow + d, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(val, ors, orow + d, 0, 0);
+    }
+}
+
+template <bool SPLIT>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   // K and V tiles, double buffered, 16 KiB each.  Four distinct objects (not offsets into one
   // array) with buffer choices fixed at compile time, so the compiler can see that the LDS-DMA
@@ -117,8 +168,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   typedef __attribute__((address_space(4))) const int32_t const_i32_t;
   const_i32_t* const work_words = (const_i32_t*)p.work;
   auto work = [&](int i) {
-    const_i32_t* w = work_words + 4 * i;
-    return WorkItem{w[0], w[1], w[2], w[3]};
+    const_i32_t* w = work_words + 8 * i;
+    return WorkItem{w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[7]};
   };
   const int i_begin = ((const_i32_t*)p.slot_begin)[blockIdx.x];
   const int i_end = ((const_i32_t*)p.slot_begin)[blockIdx.x + 1];
@@ -133,8 +184,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   const int wave_q = (wave & 1) * kWaveQ;
   const MaskSpec mask = p.mask;
   const float c = p.scale_log2;
-  const uint32_t qstride_b = (uint32_t)p.q_stride * 2u, ostride_b = (uint32_t)p.o_stride * 2u;
-  const uint32_t kstride_b = (uint32_t)p.k_stride * 2u, vstride_b = (uint32_t)p.v_stride * 2u;
+  const uint32_t qstride_b = p.q_stride_b, kstride_b = p.k_stride_b, vstride_b = p.v_stride_b;
 
   // ---- tile loads: kLoadsPerTile buffer_load...lds per lane per tile; instruction j of wave
   // `wave` fills LDS rows 16j + 4*wave .. +3 (1 KiB, lane-contiguous).  Lane writes physical chunk
@@ -193,19 +243,22 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   auto start_loads = [&](const WorkItem& w) {
     const int S = w.seq_len, kvh = w.seq_kvh & 15, q0 = w.q_block * kBlockQ;
     const TileRanges t = key_tiles(q0, min(S, q0 + kBlockQ) - 1, S, mask);
-    const half_t* qhead = p.q + (int64_t)w.seq_start * p.q_stride + (kvh * kGroup + head_in_group) * kHeadDim;
+    const int tb = w.tile_begin, t1 = w.tile_end - w.tile_begin > 1 ? tb + 1 : tb;
+    const char* qhead = reinterpret_cast<const char*>(p.q) + (uint64_t)w.seq_start * qstride_b +
+                        (kvh * kGroup + head_in_group) * kRowBytes;
     const auto rs = make_rsrc(qhead, (uint32_t)S * qstride_b);
     const uint32_t row_off = (uint32_t)(q0 + wave_q + lq) * qstride_b + 16u * hl;
 #pragma unroll
     for (int st = 0; st < 8; ++st)
       qreg[st] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(rs, row_off + 32u * st, 0, 0));
-    const char* kb = reinterpret_cast<const char*>(p.k + (int64_t)w.seq_start * p.k_stride + kvh * kHeadDim);
-    load_tile(sK0, kb, kstride_b, koff, t.at(0), S);
-    load_tile(sK1, kb, kstride_b, koff, t.at(t.count() > 1 ? 1 : 0), S);
+    const char* kb = reinterpret_cast<const char*>(p.k) + (uint64_t)w.seq_start * kstride_b + kvh * kRowBytes;
+    load_tile(sK0, kb, kstride_b, koff, t.at(tb), S);
+    load_tile(sK1, kb, kstride_b, koff, t.at(t1), S);
   };
 
-  // ---- per-item state (uniform over the workgroup except q_pos)
-  int seq_start = 0, S = 1, kvh = 0, seq = 0, wq0 = 0, wq1 = 0, q_pos = 0, ps = 0, ws = 0, ntiles = 0;
+  // ---- per-entry state (uniform over the workgroup except q_pos).  Local tile it is key tile
+  // tiles.at(t0 + it) of the item; an unsplit entry has t0 = 0 and ntiles = tiles.count().
+  int seq_start = 0, S = 1, kvh = 0, seq = 0, wq0 = 0, wq1 = 0, q_pos = 0, ps = 0, ws = 0, ntiles = 0, t0 = 0;
   TileRanges tiles{};
   const char* kbase = nullptr;
   const char* vbase = nullptr;
@@ -331,14 +384,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   // into P(it) in p_cur.  The LAST iteration computes no S(it+1); it loads the next item's Q and
   // first K tiles instead (both K buffers and qreg are free by then).
   auto body = [&](auto bconst, int it, f16x (&s_cur)[2], f16x (&s_nxt)[2], h8 (&p_cur)[4],
-                  const h8 (&p_prev)[4], bool with_pv, bool has_next, const WorkItem& next) {
+                  const h8 (&p_prev)[4], bool with_pv, int next_index) {
     constexpr int B = decltype(bconst)::value;
     const bool last = it == ntiles - 1;
     char* const kfree = B == 0 ? sK0 : sK1;
     char* const knext = B == 0 ? sK1 : sK0;
     char* const vfree = B == 0 ? sV0 : sV1;
     char* const vprev = B == 0 ? sV1 : sV0;
-    const int kb = tiles.at(it) * kTileK;
+    const int kb = tiles.at(t0 + it) * kTileK;
     // Loads issued last iteration have landed and every wavefront is done with last
     // iteration's reads of the buffers about to be refilled.  Iteration 0 issued nothing since
     // the item's start; only the previous item's O stores may still be in flight then.
@@ -347,12 +400,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     else
       wait_vmcnt<kStoreOps>();
     __syncthreads();
-    if (it + 2 < ntiles) load_tile(kfree, kbase, kstride_b, koff, tiles.at(it + 2), S);
-    load_tile(vfree, vbase, vstride_b, voff, tiles.at(it), S);
+    if (it + 2 < ntiles) load_tile(kfree, kbase, kstride_b, koff, tiles.at(t0 + it + 2), S);
+    load_tile(vfree, vbase, vstride_b, voff, tiles.at(t0 + it), S);
     // The slot's last item re-loads its own Q / K(0) / K(1) as the "next" item (valid
     // addresses, never used), so every path issues the same vector-memory instruction count and
     // the waits below stay exact.
-    if (last) start_loads(next);
+    if (last) start_loads(work(next_index));
     if (!tile_full(kb, wq0, wq1, S, mask)) apply_mask(s_cur, kb);
     if (!last) {
       qk(knext, s_nxt);
@@ -382,44 +435,28 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   // The item's last PV and its output rows.  O = O^T / l; lane pair (l, l^32) holds row q_pos,
   // dims 32db + 8g + 4hl + 0..3; one permlane32 swap per dword leaves each lane 8 consecutive
   // dims (16 B): g = 2gp in the low half-wave, g = 2gp+1 in the high one.
-  auto epilogue = [&]() {
-    const float l_tot = pair_sum(l_run);
-    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    const int head = kvh * kGroup + head_in_group;
-    const auto ors = make_rsrc(p.o + (int64_t)seq_start * p.o_stride + head * kHeadDim, (uint32_t)S * ostride_b);
-    const auto lrs = make_rsrc(p.o_last + (int64_t)seq * (kQHeads * kHeadDim) + head * kHeadDim,
-                               p.o_last ? kRowBytes : 0u);
-    // Rows past the sequence (and every row but the last, for o_last) get an offset beyond the
-    // resource, so their stores are dropped; S * ostride_b < 2^31 is validated on the host.
-    const uint32_t orow = (q_pos < S ? (uint32_t)q_pos * ostride_b : 0x80000000u) + 16u * hl;
-    const uint32_t lrow = (q_pos == S - 1 ? 0u : 0x80000000u) + 16u * hl;
-    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  // Chunk of a split item: store this chunk's partial softmax state (per lane: O, m, l) for the
+  // merge kernel that runs after this launch; the chunk writes no output rows itself.
+  // kPartialRecords (>= kStoreOps) vector stores, so the next entry's wait stays exact.
+  auto write_partial = [&](const WorkItem& w) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    f4* rec = partial_records(p.partials, (w.part >> 8) + (w.part & 15), wave, lane);
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int gp = 0; gp < 2; ++gp) {
-        const f16x& v = o[db];
-        const int ga = 4 * (2 * gp), gb = 4 * (2 * gp + 1);
-        const uint32_t a0 = pack2(v[ga] * inv, v[ga + 1] * inv), a1 = pack2(v[ga + 2] * inv, v[ga + 3] * inv);
-        const uint32_t b0 = pack2(v[gb] * inv, v[gb + 1] * inv), b1 = pack2(v[gb + 2] * inv, v[gb + 3] * inv);
-        const auto r0 = __builtin_amdgcn_permlane32_swap(a0, b0, false, false);
-        const auto r1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
-        const u4 val = {r0[0], r1[0], r0[1], r1[1]};
-        const uint32_t d = 2u * (32 * db + 16 * gp);  // + 16 hl, already in orow / lrow
-        __builtin_amdgcn_raw_buffer_store_b128(val, lrs, lrow + d, 0, 0);
-        __builtin_amdgcn_raw_buffer_store_b128(val, ors, orow + d, 0, 0);
-      }
+      for (int g = 0; g < 4; ++g)
+        rec[64 * (4 * db + g)] = f4{o[db][4 * g], o[db][4 * g + 1], o[db][4 * g + 2], o[db][4 * g + 3]};
+    rec[64 * 16] = f4{m_run, l_run, 0.f, 0.f};
   };
 
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
 
-  WorkItem cur = work(i_begin);
-  start_loads(cur);
+  start_loads(work(i_begin));
   __builtin_amdgcn_s_waitcnt(0);
   for (int wi = i_begin; wi < i_end; ++wi) {
-    const bool has_next = wi + 1 < i_end;
-    const WorkItem next = work(has_next ? wi + 1 : wi);
+    const WorkItem cur = work(wi);
+    const int next_index = wi + 1 < i_end ? wi + 1 : wi;
     seq_start = cur.seq_start;
     S = cur.seq_len;
     kvh = cur.seq_kvh & 15;
@@ -431,9 +468,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     ps = min(S, mask.prefix);
     ws = min(S, mask.window);
     tiles = key_tiles(blk_q0, min(S, blk_q0 + kBlockQ) - 1, S, mask);
-    ntiles = tiles.count();
-    kbase = reinterpret_cast<const char*>(p.k + (int64_t)seq_start * p.k_stride + kvh * kHeadDim);
-    vbase = reinterpret_cast<const char*>(p.v + (int64_t)seq_start * p.v_stride + kvh * kHeadDim);
+    t0 = cur.tile_begin;
+    ntiles = cur.tile_end - cur.tile_begin;
+    kbase = reinterpret_cast<const char*>(p.k) + (uint64_t)seq_start * kstride_b + kvh * kRowBytes;
+    vbase = reinterpret_cast<const char*>(p.v) + (uint64_t)seq_start * vstride_b + kvh * kRowBytes;
 #pragma unroll
     for (int db = 0; db < 4; ++db) o[db] = f16x{};
     m_run = -INFINITY;
@@ -445,16 +483,65 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     __syncthreads();
     qk(sK0, sA);
 
-    body(I0{}, 0, sA, sB, pA, pB, false, has_next, next);
+    body(I0{}, 0, sA, sB, pA, pB, false, next_index);
     for (int it = 1; it < ntiles; it += 2) {
-      body(I1{}, it, sB, sA, pB, pA, true, has_next, next);
-      if (it + 1 < ntiles) body(I0{}, it + 1, sA, sB, pA, pB, true, has_next, next);
+      body(I1{}, it, sB, sA, pB, pA, true, next_index);
+      if (it + 1 < ntiles) body(I0{}, it + 1, sA, sB, pA, pB, true, next_index);
     }
-    epilogue();
-    cur = next;
+    if (!SPLIT || cur.split < 0)
+      store_rows(p, o, l_run, seq_start, S, seq, kvh * kGroup + head_in_group, q_pos, hl);
+    else
+      write_partial(cur);
   }
   // The last item's unused prefetch (LDS-DMA included) lands before the workgroup leaves.
   __builtin_amdgcn_s_waitcnt(0);
+}
+
+// Merge of split items (after attn_fwd_kernel, same stream): one workgroup per split item, laid
+// out like the attention kernel (wave = head of the group x 32-row half, lane = query row x
+// half of the MFMA K slots).  Each lane combines its rows' partial states in chunk order --
+// m = max_c m_c, O = sum_c 2^(m_c - m) O_c, l likewise (a chunk with no key for the row has
+// m_c = -inf and weighs 0) -- and stores the output rows like an unsplit item.  The next chunk's
+// records load while the current one accumulates.
+__global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnParams p) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(4))) const int32_t const_i32_t;
+  const_i32_t* sw = (const_i32_t*)p.splits + 8 * blockIdx.x;
+  const WorkItem w{sw[0], sw[1], sw[2], sw[3], sw[4], sw[5], sw[6], sw[7]};
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, lq = lane & 31, hl = lane >> 5;
+  const int nchunks = (w.part >> 4) & 15, first = w.part >> 8;
+  float m = -INFINITY;
+  for (int c = 0; c < nchunks; ++c) m = fmaxf(m, partial_records(p.partials, first + c, wave, lane)[64 * 16][0]);
+  f16x o[4] = {};
+  float l = 0.f;
+  f4 cur[17], nxt[17];
+  auto fetch = [&](int c, f4 (&dst)[17]) {
+    const f4* rec = partial_records(p.partials, first + c, wave, lane);
+#pragma unroll
+    for (int r = 0; r < 17; ++r) dst[r] = rec[64 * r];
+  };
+  fetch(0, cur);
+  for (int c = 0; c < nchunks; ++c) {
+    if (c + 1 < nchunks) fetch(c + 1, nxt);
+    const float f = cur[16][0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(cur[16][0] - m);
+    l += f * cur[16][1];
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[r >> 2][4 * (r & 3) + e] += f * cur[r][e];
+#pragma unroll
+    for (int r = 0; r < 17; ++r) cur[r] = nxt[r];
+  }
+  const int q_pos = w.q_block * kBlockQ + (wave & 1) * kWaveQ + lq;
+  store_rows(p, o, l, w.seq_start, w.seq_len, w.seq_kvh >> 4, (w.seq_kvh & 15) * kGroup + (wave >> 1), q_pos, hl);
+}
+
+hipError_t launch_attn_merge(const AttnParams& p, hipStream_t stream) {
+  if (p.n_splits <= 0) return hipSuccess;
+  hipLaunchKernelGGL(attn_merge_kernel, dim3(p.n_splits), dim3(kThreads), 0, stream, p);
+  return hipGetLastError();
 }
 
 // Retained-key bitmask of one sequence through the kernel's own key iteration (kept_keys_row):
@@ -467,7 +554,29 @@ __global__ void debug_mask_kernel(int S, MaskSpec mask, uint32_t* bits, int word
 
 hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream) {
   if (p.n_slots <= 0) return hipSuccess;
-  hipLaunchKernelGGL(attn_fwd_kernel, dim3(p.n_slots), dim3(kThreads), 0, stream, p);
+  // Plans without split items run the variant without the partial-result path (fewer live
+  // registers in the tile loop).
+  if (p.n_splits > 0)
+    hipLaunchKernelGGL(attn_fwd_kernel<true>, dim3(p.n_slots), dim3(kThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL(attn_fwd_kernel<false>, dim3(p.n_slots), dim3(kThreads), 0, stream, p);
+  return hipGetLastError();
+}
+
+// XCD (XCC) of each workgroup of a launch shaped like the attention kernel's (256 threads,
+// 64 KiB LDS): out[b] = hardware XCC_ID of workgroup b.
+__global__ __launch_bounds__(kThreads, 2) void xcd_map_kernel(int* out) {
+  __shared__ char lds[kTileBytes * 4];
+  unsigned x;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+  lds[threadIdx.x] = 0;
+  __syncthreads();
+  if (threadIdx.x == 0) out[blockIdx.x] = (int)(x & 0xf) + lds[1];
+}
+
+hipError_t launch_xcd_map(int* out, int n, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(xcd_map_kernel, dim3(n), dim3(kThreads), 0, stream, out);
   return hipGetLastError();
 }
 

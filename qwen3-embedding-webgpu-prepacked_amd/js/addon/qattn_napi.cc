@@ -341,6 +341,7 @@ bool read_desc(napi_env env, napi_value d, qattn_run_desc* desc, std::vector<int
   desc->mask = (int32_t)num("mask", QATTN_MASK_PREFIX_LOCAL);
   desc->prefix = (int32_t)num("prefix", 176);
   desc->window = (int32_t)num("window", 432);
+  desc->flags = (int32_t)num("flags", 0);
   if (!prop(env, d, "cuSeqlens", &v) || !get_i32_array(env, v, cu) || cu->size() < 2) {
     napi_throw_type_error(env, nullptr, "cuSeqlens must be an Int32Array of nseq+1 offsets");
     return false;
@@ -365,6 +366,7 @@ napi_value info_object(napi_env env, const qattn_run_info& i) {
   set("blockQueries", i.block_queries);
   set("tilePairs", (double)i.tile_pairs);
   set("slots", i.slots);
+  set("splitItems", i.split_items);
   return out;
 }
 
@@ -427,7 +429,7 @@ napi_value RunInfo(napi_env env, napi_callback_info info) {
   return info_object(env, i);
 }
 
-// planDescribe(desc) -> {items: Int32Array (n*4), info}; host only, no device needed.
+// planDescribe(desc) -> {items: Int32Array (n*8 entries), info}; host only, no device needed.
 napi_value PlanDescribe(napi_env env, napi_callback_info info) {
   napi_value argv[1];
   if (!args_of(env, info, 1, argv)) return nullptr;
@@ -440,12 +442,12 @@ napi_value PlanDescribe(napi_env env, napi_callback_info info) {
   if (rc) return throw_qattn(env, rc, nullptr);
   napi_value ab, arr, out;
   void* data = nullptr;
-  NAPI_OK(env, napi_create_arraybuffer(env, (size_t)n * 16, &data, &ab));
+  NAPI_OK(env, napi_create_arraybuffer(env, (size_t)n * 32, &data, &ab));
   if (n) {
     rc = qattn_plan_describe(&desc, static_cast<int32_t*>(data), n, &n, nullptr);
     if (rc) return throw_qattn(env, rc, nullptr);
   }
-  NAPI_OK(env, napi_create_typedarray(env, napi_int32_array, (size_t)n * 4, ab, 0, &arr));
+  NAPI_OK(env, napi_create_typedarray(env, napi_int32_array, (size_t)n * 8, ab, 0, &arr));
   NAPI_OK(env, napi_create_object(env, &out));
   NAPI_OK(env, napi_set_named_property(env, out, "items", arr));
   NAPI_OK(env, napi_set_named_property(env, out, "info", info_object(env, i)));

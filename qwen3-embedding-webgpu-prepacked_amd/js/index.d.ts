@@ -48,12 +48,14 @@ export class DeviceContext {
 
 export interface RunInfo {
   tokens: number; pairs: number; flops: number; bytes: number;
-  workItems: number; blockQueries: number; tilePairs: number; slots: number;
+  workItems: number; blockQueries: number; tilePairs: number; slots: number; splitItems: number;
 }
 export interface AttentionRun { handle: unknown; info: RunInfo; cuSeqlens: Int32Array }
 export interface VarlenOptions {
   queryStride?: number; keyStride?: number; valueStride?: number; outputStride?: number;
   valueOffset?: number; mask?: MaskName; prefix?: number; window?: number; lastRows?: DeviceBuffer;
+  /** Never split an item across workgroups: results independent of batch composition. */
+  batchInvariant?: boolean;
 }
 
 export class CausalAttentionKernel {
@@ -70,6 +72,8 @@ export class CausalAttentionKernel {
 export interface HipRuntimeOptions {
   device?: number; context?: DeviceContext; layers?: number; mask?: MaskName;
   prefix?: number; window?: number; seed?: number;
+  /** Default true: embeddings are bitwise independent of batching (no split-K). */
+  batchInvariant?: boolean;
 }
 export class HipAttentionRuntime implements EmbeddingRuntime {
   constructor(options?: HipRuntimeOptions);

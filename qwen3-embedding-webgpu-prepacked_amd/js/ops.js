@@ -74,6 +74,7 @@ class CausalAttentionKernel {
       mask: maskCode(options.mask || 'prefix-local'),
       prefix: options.prefix === undefined ? 176 : options.prefix,
       window: options.window === undefined ? 432 : options.window,
+      flags: options.batchInvariant ? 1 : 0,
     };
     if (options.lastRows) desc.oLast = options.lastRows.handle;
     const addon = this.context.addon;

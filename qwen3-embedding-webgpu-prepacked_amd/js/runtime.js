@@ -72,6 +72,7 @@ class HipAttentionPlan {
     this.ids.write(Int32Array.from(ids));
     const run = rt.attention.createVarlenRun(this.q, this.k, this.v, this.o, cu, {
       mask: rt.mask, prefix: rt.prefix, window: rt.window, lastRows: this.last,
+      batchInvariant: rt.batchInvariant,
     });
     try {
       for (let layer = 0; layer < rt.layers; layer += 1) {
@@ -107,6 +108,9 @@ class HipAttentionRuntime {
     this.prefix = options.prefix === undefined ? 176 : options.prefix;
     this.window = options.window === undefined ? 432 : options.window;
     this.seed = options.seed === undefined ? 0 : options.seed;
+    // Like the reference, a request's embedding does not depend on what it was batched with
+    // (bitwise); batchInvariant: false lets the planner split long items across workgroups.
+    this.batchInvariant = options.batchInvariant === undefined ? true : !!options.batchInvariant;
     this.packing = 'varlen';
     this.plans = [];
   }

@@ -18,6 +18,7 @@ HEADER_PATH = os.path.join(REPO_DIR, "include", "qattn.h")
 
 OK, EINVAL, EHIP, ENOMEM, ENODEV = 0, -1, -2, -3, -4
 MASK_CAUSAL, MASK_PREFIX_LOCAL = 0, 1
+FLAG_BATCH_INVARIANT = 1  # qattn_run_flags
 HQ, HKV, HD = 16, 8, 128
 
 
@@ -36,7 +37,7 @@ class RunDesc(ctypes.Structure):
         ("v_offset", ctypes.c_int64),
         ("cu_seqlens", ctypes.c_void_p), ("nseq", ctypes.c_int32),
         ("mask", ctypes.c_int32), ("prefix", ctypes.c_int32), ("window", ctypes.c_int32),
-        ("o_last", ctypes.c_void_p),
+        ("o_last", ctypes.c_void_p), ("flags", ctypes.c_int32),
     ]
 
 
@@ -45,7 +46,7 @@ class RunInfo(ctypes.Structure):
         ("tokens", ctypes.c_int64), ("pairs", ctypes.c_int64), ("flops", ctypes.c_int64),
         ("bytes", ctypes.c_int64), ("work_items", ctypes.c_int32),
         ("block_queries", ctypes.c_int32), ("tile_pairs", ctypes.c_int64),
-        ("slots", ctypes.c_int32), ("reserved", ctypes.c_int32),
+        ("slots", ctypes.c_int32), ("split_items", ctypes.c_int32),
     ]
 
     def as_dict(self):
@@ -90,6 +91,7 @@ def lib():
         "qattn_plan_describe": (ctypes.c_int, [ctypes.POINTER(RunDesc), vp, i32,
                                                ctypes.POINTER(i32), ctypes.POINTER(RunInfo)]),
         "qattn_plan_slots": (ctypes.c_int, [ctypes.POINTER(RunDesc), i32, vp, i32, ctypes.POINTER(i32)]),
+        "qattn_debug_xcd_map": (ctypes.c_int, [vp, i32, vp]),
         "qattn_prefill": (ctypes.c_int, [vp, ctypes.POINTER(RunDesc), vp]),
         "qattn_debug_mask": (ctypes.c_int, [vp, i32, i32, i32, i32, vp]),
         "qattn_plan_mask": (ctypes.c_int, [i32, i32, i32, i32, vp]),
@@ -124,12 +126,12 @@ def _np_ptr(a):
 
 def make_desc(q, k, v, o, cu_seqlens, mask=MASK_PREFIX_LOCAL, prefix=176, window=432,
               q_row_stride=HQ * HD, k_row_stride=HKV * HD, v_row_stride=HKV * HD,
-              o_row_stride=HQ * HD, v_offset=0, o_last=None):
+              o_row_stride=HQ * HD, v_offset=0, o_last=None, flags=0):
     """Build a qattn_run_desc.  q/k/v/o/o_last are device addresses (int).  The returned desc
     keeps a reference to its cu_seqlens array."""
     cu = np.ascontiguousarray(cu_seqlens, dtype=np.int32)
     d = RunDesc(q, k, v, o, q_row_stride, k_row_stride, v_row_stride, o_row_stride, v_offset,
-                cu.ctypes.data, len(cu) - 1, mask, prefix, window, o_last)
+                cu.ctypes.data, len(cu) - 1, mask, prefix, window, o_last, flags)
     d._cu = cu
     return d
 
@@ -144,11 +146,11 @@ def plan_slots(desc, max_slots=0):
 
 
 def plan_describe(desc):
-    """Host-only planner: (work items int32[n,4] grouped by slot, RunInfo)."""
+    """Host-only planner: (work entries int32[n,8] grouped by slot, RunInfo)."""
     n = ctypes.c_int32(0)
     info = RunInfo()
     _check(lib().qattn_plan_describe(ctypes.byref(desc), None, 0, ctypes.byref(n), ctypes.byref(info)))
-    items = np.zeros((n.value, 4), dtype=np.int32)
+    items = np.zeros((n.value, 8), dtype=np.int32)
     if n.value:
         _check(lib().qattn_plan_describe(ctypes.byref(desc), _np_ptr(items), n.value,
                                          ctypes.byref(n), None))
@@ -292,6 +294,12 @@ class Context:
         out = np.zeros((L, words), dtype=np.uint32)
         _check(lib().qattn_debug_mask(self.handle, L, mask, prefix, window,
                                       _np_ptr(out) if L else None), self.handle)
+        return out
+
+    def xcd_map(self, n=512):
+        """XCD of each of n workgroups of an attention-shaped launch (diagnostic)."""
+        out = np.zeros(n, dtype=np.int32)
+        _check(lib().qattn_debug_xcd_map(self.handle, n, _np_ptr(out)), self.handle)
         return out
 
     def qk_norm_rope(self, x_ptr, row_stride, col0, heads, cu_seqlens, weight_ptr=None,

@@ -129,7 +129,11 @@ test('N-API addon loads; host-side planning and validation work without a GPU', 
   assert.strictEqual(plan.info.tokens, 550);
   assert.strictEqual(plan.info.pairs, 1275 + 125250);
   assert.strictEqual(plan.info.workItems, 8 * (1 + 8));
-  assert.strictEqual(plan.items.length, plan.info.workItems * 4);
+  assert.strictEqual(plan.info.slots, 8 * 9);  // 9 items per KV head on 9 slots; long ones split
+  assert.ok(plan.items.length > plan.info.workItems * 8 && plan.info.splitItems > 0);
+  const inv = addon.planDescribe({ q: 1, k: 1, v: 1, o: 1, cuSeqlens: new Int32Array([0, 50, 550]), flags: 1 });
+  assert.strictEqual(inv.items.length, inv.info.workItems * 8);  // batch-invariant: whole items
+  assert.strictEqual(inv.info.splitItems, 0);
   assert.throws(() => addon.planDescribe({ q: 1, k: 1, v: 1, o: 1, cuSeqlens: new Int32Array([0, 5, 3]) }), /non-decreasing/);
   assert.throws(() => addon.planDescribe({ q: 1, k: 1, v: 1, o: 1, cuSeqlens: new Int32Array([0, 5]), mask: 1, prefix: 0, window: 0 }), /both 0/);
 });

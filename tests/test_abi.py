@@ -45,37 +45,56 @@ def test_create_without_gpu_fails_cleanly(qattn):
 
 
 @pytest.mark.parametrize("lengths,mask", [([50], 1), ([500] * 16, 1), ([5000], 1), ([1500], 1),
-                                          ([10, 150, 64, 65, 1], 0), ([5000] * 4, 1), ([500] * 16, 0)])
-def test_planner_covers_every_block_once_in_balanced_slots(qattn, oracle, lengths, mask):
+                                          ([10, 150, 64, 65, 1], 0), ([5000] * 4, 1), ([500] * 16, 0),
+                                          ([3000, 700, 9000], 1), ([2048] * 3, 0)])
+def test_planner_covers_every_tile_once_in_balanced_slots(qattn, oracle, lengths, mask):
     d = _desc(qattn, lengths, mask)
-    items, info = qattn.plan_describe(d)
+    entries, info = qattn.plan_describe(d)
     slots = qattn.plan_slots(d)
     want = {(int(np.sum(lengths[:s])), L, qb, (s << 4) | g)
             for s, L in enumerate(lengths) for qb in range((L + 63) // 64) for g in range(8)}
-    got = [tuple(int(x) for x in it) for it in items]
-    assert len(got) == len(want) == info.work_items
-    assert set(got) == want
+    got = [tuple(int(x) for x in e) for e in entries]
+    assert {e[:4] for e in got} == want and len(want) == info.work_items
+    # every item's key tiles are covered exactly once: by one whole entry, or by the chunks of
+    # one split (split >= 0) whose part fields agree (chunk ci of n, partial index first + ci)
+    by_item = {}
+    for e in got:
+        by_item.setdefault(e[:4], []).append(e)
+    splits, partials = set(), set()
+    for item, es in by_item.items():
+        n = len(_tiles(item[2], item[1], mask))
+        cover = sorted((e[4], e[5]) for e in es)
+        assert cover[0][0] == 0 and cover[-1][1] == n
+        assert all(x[1] == y[0] and x[0] < x[1] for x, y in zip(cover, cover[1:]))
+        assert cover[-1][0] < cover[-1][1]
+        if len(es) == 1:
+            assert es[0][6] == -1 and es[0][7] == 0
+            continue
+        assert len({e[6] for e in es}) == 1 and es[0][6] >= 0 and es[0][6] not in splits
+        splits.add(es[0][6])
+        parts = sorted((e[7] & 15, (e[7] >> 4) & 15, e[7] >> 8) for e in es)
+        assert [p[0] for p in parts] == list(range(len(es)))
+        assert all(p[1] == len(es) for p in parts) and len({p[2] for p in parts}) == 1
+        first = parts[0][2]
+        assert not partials & set(range(first, first + len(es)))
+        partials |= set(range(first, first + len(es)))
+    assert info.split_items == len(splits)
+    assert partials == set(range(len(partials)))
     # slot structure: offsets cover the list; slot b holds only KV heads g with g % 8 == b % 8
-    # (workgroup b runs on XCD b % 8), heaviest first; at most 512 slots (256 CUs x 2)
+    # (workgroup b runs on XCD b % 8); at most 512 slots (256 CUs x 2)
     assert slots[0] == 0 and slots[-1] == len(got) and np.all(np.diff(slots) >= 0)
     assert info.slots == len(slots) - 1 <= 512
-    cost = lambda it: 4 * len(_tiles(it[2], it[1], mask)) + 3
-    loads = np.zeros(len(slots) - 1, dtype=np.int64)
+    cost = lambda e: 4 * (e[5] - e[4]) + 3 + (4 if e[6] >= 0 else 0)
+    loads = np.array([sum(cost(e) for e in got[slots[b]:slots[b + 1]]) for b in range(len(slots) - 1)])
     for b in range(len(slots) - 1):
-        mine = got[slots[b]:slots[b + 1]]
-        assert all((it[3] & 15) % 8 == b % 8 for it in mine)
-        c = [cost(it) for it in mine]
-        assert c == sorted(c, reverse=True)
-        loads[b] = sum(c)
-    # longest-processing-time bound per XCD group: no slot exceeds the group's mean load by
-    # more than one item
+        assert all((e[3] & 15) % 8 == b % 8 for e in got[slots[b]:slots[b + 1]])
+    # balance: no slot exceeds its XCD group's mean load by more than one maximal entry
     for g in range(8):
-        grp = [it for it in got if (it[3] & 15) % 8 == g]
+        grp = [e for e in got if (e[3] & 15) % 8 == g]
         if not grp:
             continue
         used = loads[g::8][loads[g::8] > 0]
-        mean = sum(cost(it) for it in grp) / len(used)
-        assert used.max() <= mean + max(cost(it) for it in grp)
+        assert used.max() <= sum(cost(e) for e in grp) / len(used) + max(cost(e) for e in grp)
     # figures
     pairs = sum(oracle.mask_pairs(L, mask) for L in lengths)
     assert info.tokens == sum(lengths)
@@ -83,6 +102,18 @@ def test_planner_covers_every_block_once_in_balanced_slots(qattn, oracle, length
     assert info.flops == 8192 * pairs
     assert info.bytes == 12288 * sum(lengths)
     assert info.tile_pairs >= pairs
+
+
+def test_planner_splits_only_when_it_pays(qattn):
+    # 16 x 500 full causal balances exactly without splitting (q-blocks pair up to 9 tiles)
+    _, info = qattn.plan_describe(_desc(qattn, [500] * 16, 0))
+    assert info.split_items == 0
+    # 1 x 5000 sparse: 79 items per KV head on 64 slots -> some items are split
+    entries, info = qattn.plan_describe(_desc(qattn, [5000], 1))
+    assert info.split_items > 0
+    slots = qattn.plan_slots(_desc(qattn, [5000], 1))
+    loads = [sum(e[5] - e[4] for e in entries[slots[b]:slots[b + 1]]) for b in range(len(slots) - 1)]
+    assert max(loads) <= 16  # tiles per slot, against 22 for whole items
 
 
 def test_planner_slot_count_follows_the_limit(qattn):
@@ -107,7 +138,7 @@ def _tiles(qb, L, mask, P=176, W=432):
 def test_planner_sparse_tile_count_closed_form(qattn):
     # 1 x 5000, prefix 176 / window 432, 64-key tiles: block qb (rows 64qb..64qb+63) visits the
     # 3 prefix tiles plus tiles floor((64qb-431)/64) .. qb.
-    items, info = qattn.plan_describe(_desc(qattn, [5000]))
+    entries, info = qattn.plan_describe(_desc(qattn, [5000]))
     assert info.work_items == 79 * 8
     assert info.pairs == 2855472
     # every block past the prefix region visits at most 3 + 8 + 1 tiles

@@ -40,7 +40,7 @@ class Case:
     """Device copies of one packed batch and a run over it."""
 
     def __init__(self, ctx, qattn, q, k, v, cu, mask=1, prefix=176, window=432, v_layout="compact",
-                 o_last=False):
+                 o_last=False, flags=0):
         self.ctx, self.qattn = ctx, qattn
         T = int(cu[-1])
         self.T, self.cu = T, cu
@@ -59,7 +59,7 @@ class Case:
         self.lbuf = self._alloc((len(cu) - 1) * 4096) if o_last else None
         self.desc = qattn.make_desc(self.qbuf.ptr, self.kbuf.ptr, self.vbuf.ptr, self.obuf.ptr, cu,
                                     mask, prefix, window, v_row_stride=vstride, v_offset=voff,
-                                    o_last=self.lbuf.ptr if o_last else None)
+                                    o_last=self.lbuf.ptr if o_last else None, flags=flags)
 
     def _up(self, a):
         b = self.ctx.upload(a)
@@ -238,19 +238,60 @@ def test_qkvraw_value_layout_and_o_last(ctx, qattn, oracle):
 
 
 def test_varlen_equals_solo_and_isolation(ctx, qattn, oracle):
+    # Batch-invariant plans (no split-K): a sequence gives bitwise the same rows alone or packed,
+    # and other sequences' keys / values never reach it.
     lengths = [120, 700, 33]
     cu = cu_of(lengths)
     q, k, v = oracle.gen_qkv(2, 1, cu)
-    packed = Case(ctx, qattn, q, k, v, cu).run()
+    inv = qattn.FLAG_BATCH_INVARIANT
+    packed = Case(ctx, qattn, q, k, v, cu, flags=inv).run()
     s, e = int(cu[1]), int(cu[2])
-    solo = Case(ctx, qattn, q[s:e].copy(), k[s:e].copy(), v[s:e].copy(), cu_of([700])).run()
+    solo = Case(ctx, qattn, q[s:e].copy(), k[s:e].copy(), v[s:e].copy(), cu_of([700]), flags=inv).run()
     assert np.array_equal(packed[s:e], solo)
     rng = np.random.default_rng(0)
     k2, v2 = k.copy(), v.copy()
     k2[:s] = rng.integers(0, 0x3C00, k2[:s].shape, dtype=np.uint16)
     v2[e:] = rng.integers(0, 0x3C00, v2[e:].shape, dtype=np.uint16)
-    pert = Case(ctx, qattn, q, k2, v2, cu).run()
-    assert np.array_equal(pert[s:e], packed[s:e])
+    pert = Case(ctx, qattn, q, k2, v2, cu).run()   # split-K allowed: isolation still holds
+    assert np.array_equal(pert[s:e], Case(ctx, qattn, q, k, v, cu).run()[s:e])
+
+
+def test_workgroups_reach_xcds_round_robin(ctx):
+    # The planner keeps every KV head's entries on slots b with one value of b % 8 and expects
+    # round-robin dispatch to put them on one XCD, so the head's K/V tiles share one L2.
+    xcd = ctx.xcd_map(1024)
+    n = len(set(xcd.tolist()))
+    assert 8 % n == 0, xcd[:16]
+    assert all(xcd[b] == xcd[b % 8] for b in range(1024)), xcd[:32]
+
+
+def test_split_k_and_batch_invariant_plans(ctx, qattn, oracle):
+    # 1 x 5000 sparse: the default plan splits long items over several workgroups (chunks merged
+    # by the last finisher); the batch-invariant plan does not.  Both meet the bar on every
+    # 7th row (every chunk boundary lies inside the sampled blocks), agree with each other to a
+    # few fp16 ulps, and the batch-invariant rows equal the same sequence packed with others.
+    cu = cu_of([5000])
+    q, k, v = oracle.gen_qkv(5, 3, cu)
+    split = Case(ctx, qattn, q, k, v, cu)
+    whole = Case(ctx, qattn, q, k, v, cu, flags=qattn.FLAG_BATCH_INVARIANT)
+    assert qattn.plan_describe(split.desc)[1].split_items > 0
+    assert qattn.plan_describe(whole.desc)[1].split_items == 0
+    a, b = split.run(), whole.run()
+    assert np.array_equal(a, split.run())  # split plans are deterministic
+    rows = np.arange(0, 5000, 7)
+    exact = oracle.attention_exact(q, k, v, cu, rows=rows)
+    compare(a[rows], exact, "1x5000 split-K")
+    compare(b[rows], exact, "1x5000 batch-invariant")
+    assert np.abs(f16(a) - f16(b)).max() <= 2e-3
+    lengths = [300, 5000, 64]
+    cu2 = cu_of(lengths)
+    q2 = np.concatenate([oracle.gen_qkv(5, 4, cu_of([300]))[0], q, oracle.gen_qkv(5, 5, cu_of([64]))[0]])
+    k2 = np.concatenate([oracle.gen_qkv(5, 4, cu_of([300]))[1], k, oracle.gen_qkv(5, 5, cu_of([64]))[1]])
+    v2 = np.concatenate([oracle.gen_qkv(5, 4, cu_of([300]))[2], v, oracle.gen_qkv(5, 5, cu_of([64]))[2]])
+    packed = Case(ctx, qattn, q2, k2, v2, cu2, flags=qattn.FLAG_BATCH_INVARIANT).run()
+    assert np.array_equal(packed[300:5300], b)
+    for c in (split, whole):
+        c.free()
 
 
 def test_run_reuse_rebind_and_determinism(ctx, qattn, oracle):
