@@ -129,6 +129,6 @@ struct WorkItem {
   int split;
   int part;
 };
-constexpr int kMaxChunks = 15;  // nchunks fits 4 bits
+constexpr int kMaxChunks = 8;  // chunks per split item (the merge kernel takes up to 8 per pass)
 
 }  // namespace qattn

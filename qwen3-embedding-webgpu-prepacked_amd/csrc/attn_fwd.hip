@@ -70,11 +70,13 @@ struct AttnParams {
 constexpr int kPartialRecords = 17;
 
 // Vector-memory instructions per lane that one item's prologue loads (Q: 8 x 16 B, K tiles 0
-// and 1: kLoadsPerTile each) and that one item's epilogue stores (o_last row and O rows, 8 x 16 B
-// each, always issued: out-of-range lanes are dropped by the buffer resource).  The s_waitcnt
-// counts below rely on these being exact; vector memory operations retire in issue order.
+// and 1: kLoadsPerTile each) and that one item's epilogue stores (O rows, 8 x 16 B, plus as many
+// for the o_last row when the run has one; always issued: out-of-range lanes are dropped by the
+// buffer resource).  The s_waitcnt counts below rely on these being exact; vector memory
+// operations retire in issue order.
 constexpr int kPrefetchOps = 8 + 2 * kLoadsPerTile;
-constexpr int kStoreOps = 16;
+template <bool LAST>
+constexpr int kStoreOps = LAST ? 16 : 8;
 
 // s_waitcnt vmcnt(N) only (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
 template <int N>
@@ -121,9 +123,10 @@ __device__ inline float __attribute__((ext_vector_type(4)))* partial_records(flo
 // Output rows of one wavefront: O = O^T / l for query row q_pos (lanes l and l^32 share it,
 // dims 32db + 8g + 4hl + 0..3), fp16, into O and (for the sequence's last row) o_last.  One
 // permlane32 swap per dword leaves each lane 8 consecutive dims (16 B): g = 2gp in the low
-// half-wave, g = 2gp+1 in the high one.  Exactly kStoreOps buffer stores per lane; rows past the
-// sequence (and every row but the last, for o_last) get an offset beyond the buffer resource, so
-// their stores are dropped (S * o stride < 2^31 is validated on the host).
+// half-wave, g = 2gp+1 in the high one.  Exactly kStoreOps<LAST> buffer stores per lane; rows past
+// the sequence (and every row but the last, for o_last) get an offset beyond the buffer resource,
+// so their stores are dropped (S * o stride < 2^31 is validated on the host).
+template <bool LAST>
 __device__ inline void store_rows(const AttnParams& p, const f16x (&o)[4], float l_run, int seq_start,
                                   int S, int seq, int head, int q_pos, int hl) {
   const uint32_t ostride_b = p.o_stride_b;
@@ -148,12 +151,14 @@ __device__ inline void store_rows(const AttnParams& p, const f16x (&o)[4], float
       const auto r1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
       const u4 val = {r0[0], r1[0], r0[1], r1[1]};
       const uint32_t d = 2u * (32 * db + 16 * gp);  // + 16 hl, already in orow / lrow
-      __builtin_amdgcn_raw_buffer_store_b128(val, lrs, lrow + d, 0, 0);
+      if (LAST) __builtin_amdgcn_raw_buffer_store_b128(val, lrs, lrow + d, 0, 0);
       __builtin_amdgcn_raw_buffer_store_b128(val, ors, orow + d, 0, 0);
     }
 }
 
-template <bool SPLIT>
+// SPLIT: the plan has split items (partial-result path compiled in).  LAST: the run writes
+// o_last rows.
+template <bool SPLIT, bool LAST>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   // K and V tiles, double buffered, 16 KiB each.  Four distinct objects (not offsets into one
   // array) with buffer choices fixed at compile time, so the compiler can see that the LDS-DMA
@@ -398,7 +403,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     if (with_pv)
       __builtin_amdgcn_s_waitcnt(0);  // (gfx9 encoding 0: vmcnt/expcnt/lgkmcnt all zero)
     else
-      wait_vmcnt<kStoreOps>();
+      wait_vmcnt<kStoreOps<LAST>>();
     __syncthreads();
     if (it + 2 < ntiles) load_tile(kfree, kbase, kstride_b, koff, tiles.at(t0 + it + 2), S);
     load_tile(vfree, vbase, vstride_b, voff, tiles.at(t0 + it), S);
@@ -437,7 +442,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   // dims (16 B): g = 2gp in the low half-wave, g = 2gp+1 in the high one.
   // Chunk of a split item: store this chunk's partial softmax state (per lane: O, m, l) for the
   // merge kernel that runs after this launch; the chunk writes no output rows itself.
-  // kPartialRecords (>= kStoreOps) vector stores, so the next entry's wait stays exact.
+  // kPartialRecords (>= kStoreOps) vector stores, so the next entry's wait stays correct.
   auto write_partial = [&](const WorkItem& w) {
     typedef float f4 __attribute__((ext_vector_type(4)));
     f4* rec = partial_records(p.partials, (w.part >> 8) + (w.part & 15), wave, lane);
@@ -454,6 +459,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
 
   start_loads(work(i_begin));
   __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  qk(sK0, sA);  // S(0) of the first entry
   for (int wi = i_begin; wi < i_end; ++wi) {
     const WorkItem cur = work(wi);
     const int next_index = wi + 1 < i_end ? wi + 1 : wi;
@@ -477,19 +484,23 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     m_run = -INFINITY;
     l_run = 0.f;
 
-    // Q, K(0), K(1) of this item have landed: all but the previous item's O stores (the newest
-    // kStoreOps operations; the first item's loads were waited for above).
-    wait_vmcnt<kStoreOps>();
-    __syncthreads();
-    qk(sK0, sA);
-
+    // S(0) is in sA (computed before the loop or at the previous entry's end).
     body(I0{}, 0, sA, sB, pA, pB, false, next_index);
     for (int it = 1; it < ntiles; it += 2) {
       body(I1{}, it, sB, sA, pB, pA, true, next_index);
       if (it + 1 < ntiles) body(I0{}, it + 1, sA, sB, pA, pB, true, next_index);
     }
+    // Hand-over: the next entry's Q, K(0), K(1) (issued with this entry's last tile) have landed
+    // and every wave is past this entry's LDS reads, so the next S(0) goes to the matrix cores
+    // first and this entry's output rows are normalised and stored beside it.  (The next
+    // entry's first wait allows for these stores still being in flight.)
+    if (wi + 1 < i_end) {
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      qk(sK0, sA);
+    }
     if (!SPLIT || cur.split < 0)
-      store_rows(p, o, l_run, seq_start, S, seq, kvh * kGroup + head_in_group, q_pos, hl);
+      store_rows<LAST>(p, o, l_run, seq_start, S, seq, kvh * kGroup + head_in_group, q_pos, hl);
     else
       write_partial(cur);
   }
@@ -497,50 +508,84 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   __builtin_amdgcn_s_waitcnt(0);
 }
 
-// Merge of split items (after attn_fwd_kernel, same stream): one workgroup per split item, laid
-// out like the attention kernel (wave = head of the group x 32-row half, lane = query row x
-// half of the MFMA K slots).  Each lane combines its rows' partial states in chunk order --
-// m = max_c m_c, O = sum_c 2^(m_c - m) O_c, l likewise (a chunk with no key for the row has
-// m_c = -inf and weighs 0) -- and stores the output rows like an unsplit item.  The next chunk's
-// records load while the current one accumulates.
+// Merge of split items (after attn_fwd_kernel, same stream).  Workgroup (split item i, wave w)
+// redoes wavefront w's output rows of item i: thread 64 db + lane combines dims 32db..32db+31 of
+// lane's row -- records 4db..4db+3 of every chunk -- in chunk order: m = max_c m_c,
+// O = sum_c 2^(m_c - m) O_c, l likewise (a chunk with no key for the row has m_c = -inf and weighs
+// 0).  All of a thread's loads issue at once; the row sum pairs lanes l and l^32 as in the
+// attention kernel, so store_rows' layout applies per 32-dim block.
+constexpr int kMergeMaxChunks = 8;  // chunks merged per pass (more are folded in further passes)
 __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnParams p) {
   typedef float f4 __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(4))) const int32_t const_i32_t;
-  const_i32_t* sw = (const_i32_t*)p.splits + 8 * blockIdx.x;
+  const int item = blockIdx.x >> 2, wave = blockIdx.x & 3;
+  const_i32_t* sw = (const_i32_t*)p.splits + 8 * item;
   const WorkItem w{sw[0], sw[1], sw[2], sw[3], sw[4], sw[5], sw[6], sw[7]};
-  const int tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lane = tid & 63, lq = lane & 31, hl = lane >> 5;
+  const int db = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, lq = lane & 31, hl = lane >> 5;
   const int nchunks = (w.part >> 4) & 15, first = w.part >> 8;
-  float m = -INFINITY;
-  for (int c = 0; c < nchunks; ++c) m = fmaxf(m, partial_records(p.partials, first + c, wave, lane)[64 * 16][0]);
-  f16x o[4] = {};
-  float l = 0.f;
-  f4 cur[17], nxt[17];
-  auto fetch = [&](int c, f4 (&dst)[17]) {
-    const f4* rec = partial_records(p.partials, first + c, wave, lane);
+  float m = -INFINITY, l = 0.f;
+  f4 acc[4] = {};
+  for (int c0 = 0; c0 < nchunks; c0 += kMergeMaxChunks) {
+    f4 ml[kMergeMaxChunks], v[kMergeMaxChunks][4];
 #pragma unroll
-    for (int r = 0; r < 17; ++r) dst[r] = rec[64 * r];
-  };
-  fetch(0, cur);
-  for (int c = 0; c < nchunks; ++c) {
-    if (c + 1 < nchunks) fetch(c + 1, nxt);
-    const float f = cur[16][0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(cur[16][0] - m);
-    l += f * cur[16][1];
+    for (int c = 0; c < kMergeMaxChunks; ++c) {
+      if (c0 + c < nchunks) {
+        const f4* rec = partial_records(p.partials, first + c0 + c, wave, lane);
+        ml[c] = rec[64 * 16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r)
+        for (int g = 0; g < 4; ++g) v[c][g] = rec[64 * (4 * db + g)];
+      }
+    }
+    float mp = m;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[r >> 2][4 * (r & 3) + e] += f * cur[r][e];
+    for (int c = 0; c < kMergeMaxChunks; ++c)
+      if (c0 + c < nchunks) mp = fmaxf(mp, ml[c][0]);
+    const float rs = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mp);  // rescale earlier passes
+    l *= rs;
 #pragma unroll
-    for (int r = 0; r < 17; ++r) cur[r] = nxt[r];
+    for (int g = 0; g < 4; ++g) acc[g] *= rs;
+#pragma unroll
+    for (int c = 0; c < kMergeMaxChunks; ++c) {
+      if (c0 + c < nchunks) {
+        const float f = ml[c][0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml[c][0] - mp);
+        l += f * ml[c][1];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) acc[g] += f * v[c][g];
+      }
+    }
+    m = mp;
   }
+  // Output: the block of dims 32db..32db+31 of this wave's rows, as store_rows lays them out.
+  const float l_tot = pair_sum(l);
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  const int S = w.seq_len, head = (w.seq_kvh & 15) * kGroup + (wave >> 1);
   const int q_pos = w.q_block * kBlockQ + (wave & 1) * kWaveQ + lq;
-  store_rows(p, o, l, w.seq_start, w.seq_len, w.seq_kvh >> 4, (w.seq_kvh & 15) * kGroup + (wave >> 1), q_pos, hl);
+  const uint32_t ostride_b = p.o_stride_b;
+  const auto ors = make_rsrc(reinterpret_cast<const char*>(p.o) + (uint64_t)w.seq_start * ostride_b + head * kRowBytes,
+                             (uint32_t)S * ostride_b);
+  const auto lrs = make_rsrc(p.o_last + (int64_t)(w.seq_kvh >> 4) * (kQHeads * kHeadDim) + head * kHeadDim,
+                             p.o_last ? kRowBytes : 0u);
+  const uint32_t orow = (q_pos < S ? (uint32_t)q_pos * ostride_b : 0x80000000u) + 16u * hl;
+  const uint32_t lrow = (q_pos == S - 1 ? 0u : 0x80000000u) + 16u * hl;
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int gp = 0; gp < 2; ++gp) {
+    const f4 va = acc[2 * gp], vb = acc[2 * gp + 1];
+    const uint32_t a0 = pack2(va[0] * inv, va[1] * inv), a1 = pack2(va[2] * inv, va[3] * inv);
+    const uint32_t b0 = pack2(vb[0] * inv, vb[1] * inv), b1 = pack2(vb[2] * inv, vb[3] * inv);
+    const auto r0 = __builtin_amdgcn_permlane32_swap(a0, b0, false, false);
+    const auto r1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
+    const u4 val = {r0[0], r1[0], r0[1], r1[1]};
+    const uint32_t d = 2u * (32 * db + 16 * gp);
+    __builtin_amdgcn_raw_buffer_store_b128(val, lrs, lrow + d, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(val, ors, orow + d, 0, 0);
+  }
 }
 
 hipError_t launch_attn_merge(const AttnParams& p, hipStream_t stream) {
   if (p.n_splits <= 0) return hipSuccess;
-  hipLaunchKernelGGL(attn_merge_kernel, dim3(p.n_splits), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL(attn_merge_kernel, dim3(p.n_splits * kWaves), dim3(kThreads), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -556,10 +601,14 @@ hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream) {
   if (p.n_slots <= 0) return hipSuccess;
   // Plans without split items run the variant without the partial-result path (fewer live
   // registers in the tile loop).
-  if (p.n_splits > 0)
-    hipLaunchKernelGGL(attn_fwd_kernel<true>, dim3(p.n_slots), dim3(kThreads), 0, stream, p);
-  else
-    hipLaunchKernelGGL(attn_fwd_kernel<false>, dim3(p.n_slots), dim3(kThreads), 0, stream, p);
+  const dim3 grid(p.n_slots), block(kThreads);
+  if (p.n_splits > 0) {
+    if (p.o_last) hipLaunchKernelGGL((attn_fwd_kernel<true, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((attn_fwd_kernel<true, false>), grid, block, 0, stream, p);
+  } else {
+    if (p.o_last) hipLaunchKernelGGL((attn_fwd_kernel<false, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((attn_fwd_kernel<false, false>), grid, block, 0, stream, p);
+  }
   return hipGetLastError();
 }
 

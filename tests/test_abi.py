@@ -73,6 +73,7 @@ def test_planner_covers_every_tile_once_in_balanced_slots(qattn, oracle, lengths
         assert len({e[6] for e in es}) == 1 and es[0][6] >= 0 and es[0][6] not in splits
         splits.add(es[0][6])
         parts = sorted((e[7] & 15, (e[7] >> 4) & 15, e[7] >> 8) for e in es)
+        assert len(es) <= 8  # the merge kernel combines up to 8 chunks in one pass
         assert [p[0] for p in parts] == list(range(len(es)))
         assert all(p[1] == len(es) for p in parts) and len({p[2] for p in parts}) == 1
         first = parts[0][2]
