@@ -282,7 +282,9 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
             "traffic": traffic,
-            "kernel": "attn_fwd_kernel",
+            "traffic_note": "HBM bytes per launch (mean over the step's launches), rocprofv3 "
+                            "FETCH_SIZE x2.0 + WRITE_SIZE x1.0 (copy-calibrated), profiles/traffic.json",
+            "kernel": "attn_fwd_kernel (+ attn_merge_kernel on split-K plans)",
             "algorithmic_flops_per_step": total_flops,
             "algorithmic_bytes_per_step": total_bytes,
         },
