@@ -350,6 +350,7 @@ int plan_work(qattn_ctx* ctx, const qattn_run_desc* d, int max_slots, Plan* out,
   struct Item {
     WorkItem w;
     int ntiles;
+    int order;  // position in sequence-major order (sequence, then query block)
   };
   std::vector<Item> group_items[kXcds];
   qattn_run_info info{};
@@ -366,7 +367,8 @@ int plan_work(qattn_ctx* ctx, const qattn_run_desc* d, int max_slots, Plan* out,
       // [q0+32, q0+63] each compute every tile of the work item.
       info.tile_pairs += (int64_t)tr.count() * (q0 + kWaveQ < L ? 2 : 1) * kWaveQ * kTileK;
       for (int g = 0; g < kKVHeads; ++g)
-        group_items[g % kXcds].push_back({WorkItem{start, L, qb, (s << 4) | g, 0, tr.count(), -1, 0}, tr.count()});
+        group_items[g % kXcds].push_back({WorkItem{start, L, qb, (s << 4) | g, 0, tr.count(), -1, 0}, tr.count(),
+                                          (int)group_items[g % kXcds].size()});
       ++info.work_items;
     }
   }
@@ -437,19 +439,43 @@ int plan_work(qattn_ctx* ctx, const qattn_run_desc* d, int max_slots, Plan* out,
       }
       return *std::max_element(load.begin(), load.end());
     };
+    // Rounds plan (whole items, for L2 locality): items in sequence-major order, m per round,
+    // so the slots of an XCD work on the same few sequences at a time; within a round the
+    // heaviest items go to the least loaded slots.
+    auto rounds = [&](std::vector<Piece>* pieces) {
+      std::vector<int> seq_order(items.size());
+      for (int i = 0; i < (int)items.size(); ++i) seq_order[items[i].order] = i;
+      std::vector<int64_t> load(m, 0);
+      std::vector<int> slot_ix(m);
+      pieces->clear();
+      for (size_t r0 = 0; r0 < seq_order.size(); r0 += m) {
+        std::vector<int> its(seq_order.begin() + r0, seq_order.begin() + std::min(seq_order.size(), r0 + m));
+        std::stable_sort(its.begin(), its.end(), [&](int a, int b) { return items[a].ntiles > items[b].ntiles; });
+        for (int j = 0; j < m; ++j) slot_ix[j] = j;
+        std::stable_sort(slot_ix.begin(), slot_ix.end(), [&](int a, int b) { return load[a] < load[b]; });
+        for (size_t k = 0; k < its.size(); ++k) {
+          const int j = slot_ix[k];
+          pieces->push_back({j, its[k], 0, items[its[k]].ntiles});
+          load[j] += item_cost(items[its[k]].ntiles);
+        }
+      }
+      return *std::max_element(load.begin(), load.end());
+    };
     std::vector<Piece> best, trial;
-    int64_t best_span = -1;
+    int64_t best_span = rounds(&best);
     int best_chunks = 0;
     const int64_t lo = (total + m - 1) / m;
-    for (int64_t T = lo; T <= lo + 4 * max_tiles + 8; ++T) {
+    // LPT (whole items), then makespan-targeted split-K plans; a plan must be strictly better
+    // than the rounds plan to replace it.
+    for (int64_t T = lo; T <= lo + 4 * max_tiles + 8 && best_span > lo; ++T) {
       int nch = 0;
-      const int64_t span = greedy(T, &trial, &nch);
-      if (best_span < 0 || span < best_span || (span == best_span && nch < best_chunks)) {
+      const int64_t span = greedy(may_split ? T : INT64_MAX / 4, &trial, &nch);
+      if (span < best_span || (span == best_span && nch < best_chunks)) {
         best_span = span;
         best_chunks = nch;
         best.swap(trial);
       }
-      if (best_span <= lo || !may_split) break;
+      if (!may_split) break;
     }
     // Emit: per slot in assignment order; chunks of one item share a split id and partials.
     lists[g].assign(m, {});
