@@ -1,11 +1,13 @@
 'use strict';
 // CPU tests of the Node engine and the host side of the N-API boundary (no GPU needed).
-// The first two cases restate the reference's own engine tests
-// (tests/embedding-engine.test.ts:5-23 and :25-36) with a fake runtime and tokenizer.
+// The first three cases run the packer vectors of tests/golden/reference_vectors.json: the
+// reference's own engine tests (tests/embedding-engine.test.ts:5-23 and :25-36), with a fake
+// runtime and tokenizer, and this build's varlen packing of the same requests.
 const assert = require('assert');
 const path = require('path');
 const pkg = require(path.join(__dirname, '..', '..', 'qwen3-embedding-webgpu-prepacked_amd', 'js'));
 const { Qwen3EmbeddingEngine, packVarlen, cuSeqlensOf, loadAddon } = pkg;
+const vectors = require(path.join(__dirname, '..', 'golden', 'reference_vectors.json'));
 
 const cases = [];
 function test(name, fn) { cases.push({ name, fn }); }
@@ -22,14 +24,18 @@ test('coalesces up to 16 simultaneous requests and preserves result order', asyn
       };
     },
   };
-  const tokenizer = (text) => ({ input_ids: { tolist: () => [[Number(text)]] } });
-  const engine = new Qwen3EmbeddingEngine(runtime, tokenizer, 16);
-  const results = await Promise.all(Array.from({ length: 16 }, (_, index) => engine.embed(String(index + 1))));
-  assert.strictEqual(calls.length, 1);
-  assert.strictEqual(calls[0].batch, 16);
-  assert.strictEqual(calls[0].sequence, 2);
-  assert.deepStrictEqual(calls[0].lengths, Array(16).fill(2));
-  assert.deepStrictEqual(results.map((value) => value[0]), Array.from({ length: 16 }, (_, index) => index + 1));
+  const v = vectors.engine_coalesce;
+  const tokenizer = (text) => ({ input_ids: { tolist: () => [text.split(',').map(Number)] } });
+  const engine = new Qwen3EmbeddingEngine(runtime, tokenizer, v.max_batch);
+  assert.strictEqual(engine.eosToken, v.eos);
+  const results = await Promise.all(v.requests.map((r) => engine.embed(r.join(','))));
+  assert.strictEqual(calls.length, v.expect_calls.length);
+  calls.forEach((c, i) => {
+    assert.strictEqual(c.batch, v.expect_calls[i].batch);
+    assert.strictEqual(c.sequence, v.expect_calls[i].sequence);
+    assert.deepStrictEqual(c.lengths, v.expect_calls[i].lengths);
+  });
+  assert.deepStrictEqual(results.map((value) => value[0]), v.expect_first_ids);
 });
 
 test('pads mixed-length requests after their final token', async () => {
@@ -39,26 +45,30 @@ test('pads mixed-length requests after their final token', async () => {
       return { async run(ids) { recorded = Array.from(ids); return Array.from({ length: batch }, () => new Float32Array(1)); } };
     },
   };
+  const v = vectors.engine_pad;
   const tokenizer = (text) => ({ input_ids: { tolist: () => [text.split(',').map(Number)] } });
-  const engine = new Qwen3EmbeddingEngine(runtime, tokenizer, 16, 0, 99);
-  await Promise.all([engine.embed('1'), engine.embed('2,3')]);
-  assert.deepStrictEqual(recorded, [1, 99, 99, 2, 3, 99]);
+  const engine = new Qwen3EmbeddingEngine(runtime, tokenizer, v.max_batch, 0, v.eos);
+  await Promise.all(v.requests.map((r) => engine.embed(r.join(','))));
+  assert.deepStrictEqual(recorded, v.expect_padded_ids);
 });
 
 test('a varlen runtime receives requests packed back to back, without padding', async () => {
-  const seen = [];
-  const runtime = {
-    packing: 'varlen',
-    createPlan(batch, sequence) {
-      return { async run(ids, lengths) { seen.push({ batch, sequence, ids: Array.from(ids), lengths: Array.from(lengths) });
-        return Array.from({ length: batch }, (_, i) => new Float32Array([lengths[i]])); } };
-    },
-  };
-  const tokenizer = (text) => ({ input_ids: { tolist: () => [text.split(',').map(Number)] } });
-  const engine = new Qwen3EmbeddingEngine(runtime, tokenizer, 16, 0, 99);
-  const out = await Promise.all([engine.embed('1'), engine.embed('2,3'), engine.embed('4,5,99')]);
-  assert.deepStrictEqual(seen, [{ batch: 3, sequence: 3, ids: [1, 99, 2, 3, 99, 4, 5, 99], lengths: [2, 3, 3] }]);
-  assert.deepStrictEqual(out.map((x) => x[0]), [2, 3, 3]);
+  for (const c of vectors.varlen_pack.cases) {
+    const seen = [];
+    const runtime = {
+      packing: 'varlen',
+      createPlan(batch, sequence) {
+        return { async run(ids, lengths) { seen.push({ batch, sequence, ids: Array.from(ids), lengths: Array.from(lengths) });
+          return Array.from({ length: batch }, (_, i) => new Float32Array([lengths[i]])); } };
+      },
+    };
+    const tokenizer = (text) => ({ input_ids: { tolist: () => [text.split(',').map(Number)] } });
+    const engine = new Qwen3EmbeddingEngine(runtime, tokenizer, 16, 0, vectors.varlen_pack.eos);
+    const out = await Promise.all(c.requests.map((r) => engine.embed(r.join(','))));
+    assert.deepStrictEqual(seen, [{ batch: c.requests.length, sequence: c.sequence, ids: c.ids, lengths: c.lengths }]);
+    assert.deepStrictEqual(Array.from(cuSeqlensOf(seen[0].lengths)), c.cu_seqlens);
+    assert.deepStrictEqual(out.map((x) => x[0]), c.lengths);
+  }
 });
 
 test('more than maxBatchSize requests split into batches in arrival order; plans are cached per batch:sequence', async () => {
