@@ -338,6 +338,13 @@ struct Plan {
 int item_cost(int ntiles) { return 4 * ntiles + 3; }
 constexpr int kChunkExtra = 4;
 constexpr int kMinChunkTiles = 2;
+// Slot speeds, in time per unit of cost (per mille).  The CUs issue from their oldest wavefronts
+// first, so the second workgroup of each CU (slots cu_count..2*cu_count-1: an XCD's first 32
+// workgroups take one CU each) runs its tiles about 20% slower than the first while both are
+// resident (traces: 2.34 vs 1.97 us per tile).  Weighting its load by that factor lets both
+// finish together.
+constexpr int64_t kFirstSlotTime = 1000;
+constexpr int64_t kSecondSlotTime = 1200;
 
 // The planner: validated description -> work entries grouped into slots + run figures.
 int plan_work(qattn_ctx* ctx, const qattn_run_desc* d, int max_slots, Plan* out,
@@ -394,54 +401,96 @@ int plan_work(qattn_ctx* ctx, const qattn_run_desc* d, int max_slots, Plan* out,
       total += item_cost(it.ntiles);
       max_tiles = std::max(max_tiles, it.ntiles);
     }
-    // One greedy pass for target T: per item, (slot, tile range) pieces; returns the makespan.
+    // Slot j of this group is global slot kXcds * j + g: the first half of the group's share
+    // of the launch are first workgroups on their CUs.  Loads are in cost units; finish times
+    // (load x time per unit) are what the plans balance.
+    const int first_slots = std::max(1, per_group / kBlocksPerCU);
+    std::vector<int64_t> slot_time(m);
+    for (int j = 0; j < m; ++j) slot_time[j] = j < first_slots ? kFirstSlotTime : kSecondSlotTime;
+    auto span_of = [&](const std::vector<int64_t>& load) {
+      int64_t span = 0;
+      for (int j = 0; j < m; ++j) span = std::max(span, load[j] * slot_time[j]);
+      return span;
+    };
+    // One greedy pass for target finish time T: per item, (slot, tile range) pieces; returns the
+    // makespan.
     struct Piece {
-      int slot, item, a, b;
+      int slot, item, a, b, cost;
     };
     auto greedy = [&](int64_t T, std::vector<Piece>* pieces, int* nchunks) {
       std::vector<int64_t> load(m, 0);
-      // min-heap of (load, slot)
-      std::vector<std::pair<int64_t, int>> heap;
-      for (int j = 0; j < m; ++j) heap.push_back({0, j});
-      auto cmp = [](const std::pair<int64_t, int>& x, const std::pair<int64_t, int>& y) { return x > y; };
-      std::make_heap(heap.begin(), heap.end(), cmp);
-      auto pop = [&]() { std::pop_heap(heap.begin(), heap.end(), cmp); auto t = heap.back(); heap.pop_back(); return t.second; };
-      auto push = [&](int j) { heap.push_back({load[j], j}); std::push_heap(heap.begin(), heap.end(), cmp); };
+      // One min-heap of (load, slot) per speed class: within a class the least loaded slot
+      // both finishes first and has the most room under T.
+      typedef std::pair<int64_t, int> Entry;
+      std::vector<Entry> heap[2];
+      for (int j = 0; j < m; ++j) heap[j < first_slots ? 0 : 1].push_back({0, j});
+      auto cmp = [](const Entry& x, const Entry& y) { return x > y; };
+      for (auto& h : heap) std::make_heap(h.begin(), h.end(), cmp);
+      auto top = [&](int c) { return heap[c].empty() ? -1 : heap[c].front().second; };
+      auto take_out = [&](int j) {
+        auto& h = heap[j < first_slots ? 0 : 1];
+        std::pop_heap(h.begin(), h.end(), cmp);
+        h.pop_back();
+      };
+      auto put_back = [&](int j) {
+        auto& h = heap[j < first_slots ? 0 : 1];
+        h.push_back({load[j], j});
+        std::push_heap(h.begin(), h.end(), cmp);
+      };
+      // The class top that finishes first after adding cost c.
+      auto earliest = [&](int64_t c) {
+        const int a = top(0), b = top(1);
+        if (a < 0) return b;
+        if (b < 0) return a;
+        return (load[a] + c) * slot_time[a] <= (load[b] + c) * slot_time[b] ? a : b;
+      };
+      // Room under T (cost units) of slot j.
+      auto room = [&](int j) { return T / slot_time[j] - load[j]; };
       pieces->clear();
       *nchunks = 0;
       for (int i = 0; i < (int)items.size(); ++i) {
         const int n = items[i].ntiles;
-        int j = pop();
-        if (load[j] + item_cost(n) <= T || n < 2 * kMinChunkTiles || !may_split) {
+        int j = earliest(item_cost(n));
+        if ((load[j] + item_cost(n)) * slot_time[j] <= T || n < 2 * kMinChunkTiles || !may_split) {
+          take_out(j);
           load[j] += item_cost(n);
-          pieces->push_back({j, i, 0, n});
-          push(j);
+          pieces->push_back({j, i, 0, n, item_cost(n)});
+          put_back(j);
           continue;
         }
         std::vector<Piece> mine;
         int a = 0;
         while (a < n) {
-          if (!mine.empty()) j = pop();
           const int rest = n - a;
-          // Room left under T on the least loaded slot; none: the rest goes there whole.
-          int take = (int)((T - load[j] - 3 - kChunkExtra) / 4);
+          // The class top with the most room under T takes a chunk that fills it; if no
+          // slot has room for a chunk, the rest goes whole to the slot that finishes it first.
+          const int x = top(0), y = top(1);
+          j = x < 0 ? y : y < 0 ? x : (room(x) >= room(y) ? x : y);
+          int take = (int)((room(j) - 3 - kChunkExtra) / 4);
           if (take < kMinChunkTiles || (int)mine.size() == kMaxChunks - 1 || take >= rest ||
-              rest - take < kMinChunkTiles)
+              rest - take < kMinChunkTiles) {
             take = rest;
-          mine.push_back({j, i, a, a + take});
+            j = earliest(item_cost(rest) + kChunkExtra);
+          }
+          take_out(j);
+          mine.push_back({j, i, a, a + take, item_cost(take) + kChunkExtra});
           load[j] += item_cost(take) + kChunkExtra;
-          push(j);
+          put_back(j);
           a += take;
         }
-        if (mine.size() == 1) load[mine[0].slot] -= kChunkExtra;  // not split after all
-        else *nchunks += (int)mine.size();
+        if (mine.size() == 1) {  // not split after all
+          load[mine[0].slot] -= kChunkExtra;
+          mine[0].cost -= kChunkExtra;
+        } else {
+          *nchunks += (int)mine.size();
+        }
         pieces->insert(pieces->end(), mine.begin(), mine.end());
       }
-      return *std::max_element(load.begin(), load.end());
+      return span_of(load);
     };
     // Rounds plan (whole items, for L2 locality): items in sequence-major order, m per round,
     // so the slots of an XCD work on the same few sequences at a time; within a round the
-    // heaviest items go to the least loaded slots.
+    // heaviest items go to the slots that would finish first.
     auto rounds = [&](std::vector<Piece>* pieces) {
       std::vector<int> seq_order(items.size());
       for (int i = 0; i < (int)items.size(); ++i) seq_order[items[i].order] = i;
@@ -452,22 +501,86 @@ int plan_work(qattn_ctx* ctx, const qattn_run_desc* d, int max_slots, Plan* out,
         std::vector<int> its(seq_order.begin() + r0, seq_order.begin() + std::min(seq_order.size(), r0 + m));
         std::stable_sort(its.begin(), its.end(), [&](int a, int b) { return items[a].ntiles > items[b].ntiles; });
         for (int j = 0; j < m; ++j) slot_ix[j] = j;
-        std::stable_sort(slot_ix.begin(), slot_ix.end(), [&](int a, int b) { return load[a] < load[b]; });
+        std::stable_sort(slot_ix.begin(), slot_ix.end(), [&](int a, int b) {
+          return (load[a] + 1) * slot_time[a] < (load[b] + 1) * slot_time[b];
+        });
         for (size_t k = 0; k < its.size(); ++k) {
           const int j = slot_ix[k];
-          pieces->push_back({j, its[k], 0, items[its[k]].ntiles});
+          pieces->push_back({j, its[k], 0, items[its[k]].ntiles, item_cost(items[its[k]].ntiles)});
           load[j] += item_cost(items[its[k]].ntiles);
         }
       }
-      return *std::max_element(load.begin(), load.end());
+      return span_of(load);
+    };
+    // Local search on a plan.  Slots are visited from the one that finishes last; a slot hands
+    // one of its pieces to a slot that finishes earlier, or trades it for a cheaper piece there,
+    // when both then finish before it did.  Each move lowers the sorted vector of finish times
+    // lexicographically, so the search ends; the first slots' moves lower the makespan, the
+    // others make room for later ones.  Pieces only change slots: their order (each slot's
+    // entry order and the chunk order of split items) stays.
+    auto improve = [&](std::vector<Piece>* pieces) {
+      std::vector<int64_t> load(m, 0);
+      std::vector<std::vector<int>> held(m);
+      for (int k = 0; k < (int)pieces->size(); ++k) {
+        load[(*pieces)[k].slot] += (*pieces)[k].cost;
+        held[(*pieces)[k].slot].push_back(k);
+      }
+      auto fin = [&](int j, int64_t l) { return l * slot_time[j]; };
+      std::vector<int> order(m);
+      for (int moves = 0; moves < 8 * (int)pieces->size(); ++moves) {
+        for (int j = 0; j < m; ++j) order[j] = j;
+        std::sort(order.begin(), order.end(), [&](int a, int b) { return fin(a, load[a]) > fin(b, load[b]); });
+        bool moved = false;
+        for (int oj = 0; oj < m && !moved; ++oj) {
+          const int j = order[oj];
+          const int64_t fj = fin(j, load[j]);
+          for (int ok = m - 1; ok > oj && !moved; --ok) {
+            const int k = order[ok];
+            if (fin(k, load[k]) >= fj) break;
+            for (int pi : held[j]) {
+              const int cp = (*pieces)[pi].cost;
+              int qsel = -1;
+              bool ok_move = std::max(fin(j, load[j] - cp), fin(k, load[k] + cp)) < fj;
+              if (!ok_move) {
+                for (int qi : held[k]) {
+                  const int cq = (*pieces)[qi].cost;
+                  if (cq < cp && std::max(fin(j, load[j] - cp + cq), fin(k, load[k] - cq + cp)) < fj) {
+                    qsel = qi;
+                    break;
+                  }
+                }
+                if (qsel < 0) continue;
+              }
+              auto relocate = [&](int idx, int from, int to) {
+                held[from].erase(std::find(held[from].begin(), held[from].end(), idx));
+                held[to].push_back(idx);
+                (*pieces)[idx].slot = to;
+                load[from] -= (*pieces)[idx].cost;
+                load[to] += (*pieces)[idx].cost;
+              };
+              relocate(pi, j, k);
+              if (qsel >= 0) relocate(qsel, k, j);
+              moved = true;
+              break;
+            }
+          }
+        }
+        if (!moved) break;
+      }
+      return span_of(load);
     };
     std::vector<Piece> best, trial;
     int64_t best_span = rounds(&best);
+    best_span = improve(&best);
     int best_chunks = 0;
-    const int64_t lo = (total + m - 1) / m;
+    // Lower bound of the makespan: the total cost spread over the slots in proportion to their
+    // speeds.  Targets step by a quarter tile (one cost unit) on a first slot.
+    double rate = 0.0;
+    for (int j = 0; j < m; ++j) rate += 1.0 / (double)slot_time[j];
+    const int64_t lo = (int64_t)std::ceil((double)total / rate);
     // LPT (whole items), then makespan-targeted split-K plans; a plan must be strictly better
     // than the rounds plan to replace it.
-    for (int64_t T = lo; T <= lo + 4 * max_tiles + 8 && best_span > lo; ++T) {
+    for (int64_t T = lo; T <= lo + (4 * max_tiles + 8) * kFirstSlotTime && best_span > lo; T += kFirstSlotTime) {
       int nch = 0;
       const int64_t span = greedy(may_split ? T : INT64_MAX / 4, &trial, &nch);
       if (span < best_span || (span == best_span && nch < best_chunks)) {
@@ -477,6 +590,7 @@ int plan_work(qattn_ctx* ctx, const qattn_run_desc* d, int max_slots, Plan* out,
       }
       if (!may_split) break;
     }
+    best_span = improve(&best);
     // Emit: per slot in assignment order; chunks of one item share a split id and partials.
     lists[g].assign(m, {});
     for (size_t k = 0; k < best.size();) {

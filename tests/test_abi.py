@@ -117,6 +117,28 @@ def test_planner_splits_only_when_it_pays(qattn):
     assert max(loads) <= 16  # tiles per slot, against 22 for whole items
 
 
+@pytest.mark.parametrize("lengths,mask", [([500] * 16, 0), ([5000], 1), ([5000] * 4, 1)])
+def test_planner_gives_second_workgroups_less_work(qattn, lengths, mask):
+    # Slots 256..511 are the second workgroup on their CU and run slower while the first is
+    # resident: the planner balances finish times (load x 1.2 for them), not loads.
+    d = _desc(qattn, lengths, mask)
+    entries, _ = qattn.plan_describe(d)
+    slots = qattn.plan_slots(d)
+    n = len(slots) - 1
+    assert n == 512
+
+    def cost(b):
+        es = entries[slots[b]:slots[b + 1]]
+        return sum(4 * (e[5] - e[4]) + 3 + (4 if e[6] >= 0 else 0) for e in es)
+
+    first = [cost(b) for b in range(256)]
+    second = [cost(b) for b in range(256, 512)]
+    assert np.mean(second) < np.mean(first)
+    span = max(max(first) * 1000, max(second) * 1200)
+    even = max(max(first), max(second)) * 1200  # what equal loads would give at best
+    assert span <= even
+
+
 def test_planner_slot_count_follows_the_limit(qattn):
     d = _desc(qattn, [500] * 16, 1)
     assert len(qattn.plan_slots(d, 64)) - 1 == 64
