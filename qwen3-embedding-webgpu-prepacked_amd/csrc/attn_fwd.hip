@@ -202,17 +202,20 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   const uint32_t koff = (uint32_t)r0 * kstride_b + (uint32_t)((pc ^ r0) << 4);
   const uint32_t voff = (uint32_t)r0 * vstride_b + (uint32_t)((pc ^ ((r0 & 3) << 2)) << 4);
   // Key tile `kt` of a sequence of S rows starting at `base` (kt * kTileK < S always).
-  auto load_tile = [&](char* dst, const char* base, uint32_t stride_b, uint32_t off, int kt, int S) {
+  auto tile_rsrc = [&](const char* base, uint32_t stride_b, int kt, int S) {
     const int kb = kt * kTileK;
-    const auto rs = make_rsrc(base + (int64_t)kb * stride_b, (uint32_t)(S - kb) * stride_b);
+    return make_rsrc(base + (int64_t)kb * stride_b, (uint32_t)(S - kb) * stride_b);
+  };
+  auto load_part = [&](char* dst, __amdgpu_buffer_rsrc_t rs, uint32_t stride_b, uint32_t off, int j) {
+    // The add stays here (not hoisted into four loop-invariant registers).
+    uint32_t step = (uint32_t)(16 * j) * stride_b;
+    asm volatile("" : "+s"(step));
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(dst + j * 4096 + wave * 1024), 16, off + step, 0, 0, 0);
+  };
+  auto load_tile = [&](char* dst, const char* base, uint32_t stride_b, uint32_t off, int kt, int S) {
+    const auto rs = tile_rsrc(base, stride_b, kt, S);
 #pragma unroll
-    for (int j = 0; j < kLoadsPerTile; ++j) {
-      // The add stays here (not hoisted into four loop-invariant registers).
-      uint32_t step = (uint32_t)(16 * j) * stride_b;
-      asm volatile("" : "+s"(step));
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(dst + j * 4096 + wave * 1024), 16,
-                                               off + step, 0, 0, 0);
-    }
+    for (int j = 0; j < kLoadsPerTile; ++j) load_part(dst, rs, stride_b, off, j);
   };
 
   // ---- LDS read addresses.
@@ -270,7 +273,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
 
   // S^T (64 keys x 32 queries) for the K tile in `kt`.  Lane holds S^T[key][q_pos] for
   // key = kb + 4*hl + key_off(r), r = 0..31 over (s[0], s[1]).
-  auto qk = [&](const char* kt, f16x (&s)[2]) {
+  // `step_hook(st)` runs after step st's MFMAs (the main loop issues its tile loads there, one
+  // per step, so they reach the texture unit spread out instead of in one burst per iteration).
+  auto qk = [&](const char* kt, f16x (&s)[2], auto step_hook) {
     s[0] = f16x{};
     s[1] = f16x{};
     uint32_t kx = kread_xor;
@@ -282,8 +287,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
       const h8 a1 = *reinterpret_cast<const h8*>(kt + ka + 32 * kRowBytes);
       s[0] = mfma32(a0, qreg[st], s[0]);
       s[1] = mfma32(a1, qreg[st], s[1]);
+      step_hook(st);
     }
   };
+  auto no_hook = [](int) {};
 
   // O^T (128 d x 32 q) += V^T (128 x 64 keys) . P^T.  Step t covers keys kb+16t..kb+16t+15;
   // slot j of lane half hl is key 16t + 8*(j>>2) + 4*hl + (j&3), whose probability is pf[t][j].
@@ -405,15 +412,28 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     else
       wait_vmcnt<kStoreOps<LAST>>();
     __syncthreads();
-    if (it + 2 < ntiles) load_tile(kfree, kbase, kstride_b, koff, tiles.at(t0 + it + 2), S);
-    load_tile(vfree, vbase, vstride_b, voff, tiles.at(t0 + it), S);
+    // This iteration's tile loads: K(it+2) (if any) and V(it), one instruction per S(it+1) step
+    // when there is one.
+    const bool kload = it + 2 < ntiles;
+    const auto krs = tile_rsrc(kbase, kstride_b, tiles.at(t0 + (kload ? it + 2 : it)), S);
+    const auto vrs = tile_rsrc(vbase, vstride_b, tiles.at(t0 + it), S);
+    if (last) {
+      if (kload) load_tile(kfree, kbase, kstride_b, koff, tiles.at(t0 + it + 2), S);
+      load_tile(vfree, vbase, vstride_b, voff, tiles.at(t0 + it), S);
+    }
     // The slot's last item re-loads its own Q / K(0) / K(1) as the "next" item (valid
     // addresses, never used), so every path issues the same vector-memory instruction count and
     // the waits below stay exact.
     if (last) start_loads(work(next_index));
     if (!tile_full(kb, wq0, wq1, S, mask)) apply_mask(s_cur, kb);
     if (!last) {
-      qk(knext, s_nxt);
+      qk(knext, s_nxt, [&](int st) {
+        if (st < kLoadsPerTile) {
+          if (kload) load_part(kfree, krs, kstride_b, koff, st);
+        } else {
+          load_part(vfree, vrs, vstride_b, voff, st - kLoadsPerTile);
+        }
+      });
     } else {
       // No S(it+1) on the last tile.  Defining the set anyway (cheaply) keeps its previous
       // contents from staying live across the softmax.
@@ -460,7 +480,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   start_loads(work(i_begin));
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  qk(sK0, sA);  // S(0) of the first entry
+  qk(sK0, sA, no_hook);  // S(0) of the first entry
   for (int wi = i_begin; wi < i_end; ++wi) {
     const WorkItem cur = work(wi);
     const int next_index = wi + 1 < i_end ? wi + 1 : wi;
@@ -491,18 +511,19 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
       if (it + 1 < ntiles) body(I0{}, it + 1, sA, sB, pA, pB, true, next_index);
     }
     // Hand-over: the next entry's Q, K(0), K(1) (issued with this entry's last tile) have landed
-    // and every wave is past this entry's LDS reads, so the next S(0) goes to the matrix cores
-    // first and this entry's output rows are normalised and stored beside it.  (The next
-    // entry's first wait allows for these stores still being in flight.)
+    // and every wave is past this entry's LDS reads.  This entry's output rows are normalised
+    // and stored first, then the next S(0) goes to the matrix cores: O and the next scores are
+    // never live together (the other workgroup's wavefronts keep the matrix cores busy
+    // meanwhile).  The next entry's first wait allows for these stores still being in flight.
     if (wi + 1 < i_end) {
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
-      qk(sK0, sA);
     }
     if (!SPLIT || cur.split < 0)
       store_rows<LAST>(p, o, l_run, seq_start, S, seq, kvh * kGroup + head_in_group, q_pos, hl);
     else
       write_partial(cur);
+    if (wi + 1 < i_end) qk(sK0, sA, no_hook);
   }
   // The last item's unused prefetch (LDS-DMA included) lands before the workgroup leaves.
   __builtin_amdgcn_s_waitcnt(0);
