@@ -276,8 +276,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   // `step_hook(st)` runs after step st's MFMAs (the main loop issues its tile loads there, one
   // per step, so they reach the texture unit spread out instead of in one burst per iteration).
   auto qk = [&](const char* kt, f16x (&s)[2], auto step_hook) {
-    s[0] = f16x{};
-    s[1] = f16x{};
     uint32_t kx = kread_xor;
     asm volatile("" : "+v"(kx));  // keeps the 8 addresses from being hoisted into registers
 #pragma unroll
@@ -285,8 +283,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
       const uint32_t ka = kread_base + (((uint32_t)st << 5) ^ kx);
       const h8 a0 = *reinterpret_cast<const h8*>(kt + ka);
       const h8 a1 = *reinterpret_cast<const h8*>(kt + ka + 32 * kRowBytes);
-      s[0] = mfma32(a0, qreg[st], s[0]);
-      s[1] = mfma32(a1, qreg[st], s[1]);
+      // step 0 accumulates onto the inline constant 0 (no zeroed registers)
+      s[0] = mfma32(a0, qreg[st], st == 0 ? f16x{} : s[0]);
+      s[1] = mfma32(a1, qreg[st], st == 0 ? f16x{} : s[1]);
       step_hook(st);
     }
   };
