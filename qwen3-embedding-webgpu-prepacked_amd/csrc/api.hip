@@ -332,19 +332,27 @@ struct Plan {
   int32_t partials = 0;              // chunk partial-result records the workspace holds
 };
 
-// Relative cost of a piece of work for load balancing, in quarter tiles: its key tiles plus a
-// fixed share for its start (Q and first tiles) and end (last PV, O stores) that the pipeline
-// cannot hide; a chunk of a split item also writes / merges a partial result.
-int item_cost(int ntiles) { return 4 * ntiles + 3; }
-constexpr int kChunkExtra = 4;
+// Cost model for load balancing, in quarter tiles (one 64-key tile of an entry = 4), fitted to
+// the measured duration of every workgroup of the 16x500 and 1x5000 benchmark launches (start
+// and end s_memtime of each workgroup of an instrumented build, 28 HBM-resident layers; least
+// squares over 1024 workgroups, residual 2.6%):
+//   duration = speed x (tiles + 3.3 entries + 4.6) tile times,
+// speed 1 for the first workgroup of a CU and 1.3 for the second (the CUs issue from their
+// oldest wavefronts first).  An entry's start and end (Q and first K tiles, last PV, O stores)
+// cost about three tiles that the pipeline does not hide, a workgroup's start (all launch
+// together, so their first loads queue at HBM) and end about four and a half, and a chunk of a
+// split item no more than any other entry.  Refits on other plans gave 2.2-3.3 tiles per entry
+// and 1.2-1.3 for the second workgroup; these constants measured fastest among them (16x500:
+// 37.5 us with the previous 0.75-tile entries and 1.2 factor, 35.6 us with these).
+constexpr int kEntryCost = 13;
+int item_cost(int ntiles) { return 4 * ntiles + kEntryCost; }
+constexpr int kSlotBase = 18;
+constexpr int kChunkExtra = 0;
 constexpr int kMinChunkTiles = 2;
-// Slot speeds, in time per unit of cost (per mille).  The CUs issue from their oldest wavefronts
-// first, so the second workgroup of each CU (slots cu_count..2*cu_count-1: an XCD's first 32
-// workgroups take one CU each) runs its tiles about 20% slower than the first while both are
-// resident (traces: 2.34 vs 1.97 us per tile).  Weighting its load by that factor lets both
-// finish together.
+// Slot speeds, in time per unit of cost (per mille): slots cu_count..2*cu_count-1 (an XCD's
+// first 32 workgroups take one CU each) are the second workgroups.
 constexpr int64_t kFirstSlotTime = 1000;
-constexpr int64_t kSecondSlotTime = 1200;
+constexpr int64_t kSecondSlotTime = 1300;
 
 // The planner: validated description -> work entries grouped into slots + run figures.
 int plan_work(qattn_ctx* ctx, const qattn_run_desc* d, int max_slots, Plan* out,
@@ -395,12 +403,13 @@ int plan_work(qattn_ctx* ctx, const qattn_run_desc* d, int max_slots, Plan* out,
     std::stable_sort(items.begin(), items.end(), [](const Item& a, const Item& b) { return a.ntiles > b.ntiles; });
     const int m = std::min<int>(per_group, (int)items.size());
     if (!m) continue;
-    int64_t total = 0;
+    int64_t total = 0;  // the group's cost, workgroup bases included
     int max_tiles = 0;
     for (const Item& it : items) {
       total += item_cost(it.ntiles);
       max_tiles = std::max(max_tiles, it.ntiles);
     }
+    total += (int64_t)m * kSlotBase;
     // Slot j of this group is global slot kXcds * j + g: the first half of the group's share
     // of the launch are first workgroups on their CUs.  Loads are in cost units; finish times
     // (load x time per unit) are what the plans balance.
@@ -418,7 +427,7 @@ int plan_work(qattn_ctx* ctx, const qattn_run_desc* d, int max_slots, Plan* out,
       int slot, item, a, b, cost;
     };
     auto greedy = [&](int64_t T, std::vector<Piece>* pieces, int* nchunks) {
-      std::vector<int64_t> load(m, 0);
+      std::vector<int64_t> load(m, kSlotBase);
       // One min-heap of (load, slot) per speed class: within a class the least loaded slot
       // both finishes first and has the most room under T.
       typedef std::pair<int64_t, int> Entry;
@@ -466,7 +475,7 @@ int plan_work(qattn_ctx* ctx, const qattn_run_desc* d, int max_slots, Plan* out,
           // slot has room for a chunk, the rest goes whole to the slot that finishes it first.
           const int x = top(0), y = top(1);
           j = x < 0 ? y : y < 0 ? x : (room(x) >= room(y) ? x : y);
-          int take = (int)((room(j) - 3 - kChunkExtra) / 4);
+          int take = (int)((room(j) - kEntryCost - kChunkExtra) / 4);
           if (take < kMinChunkTiles || (int)mine.size() == kMaxChunks - 1 || take >= rest ||
               rest - take < kMinChunkTiles) {
             take = rest;
@@ -494,7 +503,7 @@ int plan_work(qattn_ctx* ctx, const qattn_run_desc* d, int max_slots, Plan* out,
     auto rounds = [&](std::vector<Piece>* pieces) {
       std::vector<int> seq_order(items.size());
       for (int i = 0; i < (int)items.size(); ++i) seq_order[items[i].order] = i;
-      std::vector<int64_t> load(m, 0);
+      std::vector<int64_t> load(m, kSlotBase);
       std::vector<int> slot_ix(m);
       pieces->clear();
       for (size_t r0 = 0; r0 < seq_order.size(); r0 += m) {
@@ -519,7 +528,7 @@ int plan_work(qattn_ctx* ctx, const qattn_run_desc* d, int max_slots, Plan* out,
     // others make room for later ones.  Pieces only change slots: their order (each slot's
     // entry order and the chunk order of split items) stays.
     auto improve = [&](std::vector<Piece>* pieces) {
-      std::vector<int64_t> load(m, 0);
+      std::vector<int64_t> load(m, kSlotBase);
       std::vector<std::vector<int>> held(m);
       for (int k = 0; k < (int)pieces->size(); ++k) {
         load[(*pieces)[k].slot] += (*pieces)[k].cost;

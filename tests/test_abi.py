@@ -85,7 +85,7 @@ def test_planner_covers_every_tile_once_in_balanced_slots(qattn, oracle, lengths
     # (workgroup b runs on XCD b % 8); at most 512 slots (256 CUs x 2)
     assert slots[0] == 0 and slots[-1] == len(got) and np.all(np.diff(slots) >= 0)
     assert info.slots == len(slots) - 1 <= 512
-    cost = lambda e: 4 * (e[5] - e[4]) + 3 + (4 if e[6] >= 0 else 0)
+    cost = lambda e: 4 * (e[5] - e[4]) + 13  # the planner's cost model (quarter tiles)
     loads = np.array([sum(cost(e) for e in got[slots[b]:slots[b + 1]]) for b in range(len(slots) - 1)])
     for b in range(len(slots) - 1):
         assert all((e[3] & 15) % 8 == b % 8 for e in got[slots[b]:slots[b + 1]])
@@ -120,7 +120,7 @@ def test_planner_splits_only_when_it_pays(qattn):
 @pytest.mark.parametrize("lengths,mask", [([500] * 16, 0), ([5000], 1), ([5000] * 4, 1)])
 def test_planner_gives_second_workgroups_less_work(qattn, lengths, mask):
     # Slots 256..511 are the second workgroup on their CU and run slower while the first is
-    # resident: the planner balances finish times (load x 1.2 for them), not loads.
+    # resident: the planner balances finish times (load x 1.3 for them), not loads.
     d = _desc(qattn, lengths, mask)
     entries, _ = qattn.plan_describe(d)
     slots = qattn.plan_slots(d)
@@ -129,13 +129,13 @@ def test_planner_gives_second_workgroups_less_work(qattn, lengths, mask):
 
     def cost(b):
         es = entries[slots[b]:slots[b + 1]]
-        return sum(4 * (e[5] - e[4]) + 3 + (4 if e[6] >= 0 else 0) for e in es)
+        return 18 + sum(4 * (e[5] - e[4]) + 13 for e in es)
 
     first = [cost(b) for b in range(256)]
     second = [cost(b) for b in range(256, 512)]
     assert np.mean(second) < np.mean(first)
-    span = max(max(first) * 1000, max(second) * 1200)
-    even = max(max(first), max(second)) * 1200  # what equal loads would give at best
+    span = max(max(first) * 1000, max(second) * 1300)
+    even = max(max(first), max(second)) * 1300  # what equal loads would give at best
     assert span <= even
 
 
