@@ -151,6 +151,39 @@ def copy_calibration(mib):
     log(f"copy calibration: 5 x {mib} MiB device copies done")
 
 
+def pool_timing(reps):
+    """The consumer kernel alone (not the headline metric): qattn_pool_last_l2 over the last rows
+    of a 16 x 500 packing, at width 2048 (attention output rows) and 1024 (the reference pool's
+    hidden width, ops.ts:371), `reps` back-to-back launches each between HIP events on the
+    context stream.  One JSON line per width; algorithmic bytes = 16 rows x width x (2 + 4)."""
+    q = load_binding()
+    ctx = q.Context(0)
+    cu = np.concatenate([[0], np.cumsum([500] * 16)]).astype(np.int32)
+    T = int(cu[-1])
+    for width in (2048, 1024):
+        x, out = ctx.alloc(T * width * 2), ctx.alloc(16 * width * 4)
+        ctx.fill_normal(x.ptr, T, width, width, 7)
+        for _ in range(10):
+            ctx.pool_last_l2(x.ptr, width, width, cu, out.ptr)
+        e0, e1 = ctx.event(), ctx.event()
+        ctx.synchronize()
+        e0.record()
+        for _ in range(reps):
+            ctx.pool_last_l2(x.ptr, width, width, cu, out.ptr)
+        e1.record()
+        ctx.synchronize()
+        us = e0.elapsed_ms(e1) * 1000.0 / reps
+        nbytes = 16 * width * 6
+        print(json.dumps({"kernel": "pool_last_l2_kernel", "sequences": 16, "width": width, "launches": reps,
+                          "us_per_launch": round(us, 3), "bytes": nbytes, "GB/s": round(nbytes / us / 1e3, 2)}),
+              flush=True)
+        for b in (x, out):
+            b.free()
+        e0.destroy()
+        e1.destroy()
+    ctx.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -161,7 +194,12 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device copies of MIB MiB (torch copy_) and exit: the "
                          "known-size reference for rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
+    ap.add_argument("--pool", type=int, default=0, metavar="N",
+                    help="only time N launches of the last-token pool kernel per width and exit")
     args = ap.parse_args()
+    if args.pool:
+        pool_timing(args.pool)
+        return
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
         return

@@ -16,6 +16,7 @@
  *   QKNormRopeKernel                   ops.ts:104-166   | qattn_qk_norm_rope
  *   RoPE table                         model.ts:76-83   | built inside qattn_qk_norm_rope
  *   last-token row of poolShader       ops.ts:357       | qattn_run_desc.o_last
+ *   LastTokenPoolKernel (L2 norm)      ops.ts:347-379   | qattn_pool_last_l2
  *
  * Fixed model geometry (model.ts:18-23, ops.ts:196): 16 query heads, 8 KV heads (query head h
  * reads KV head h/2), head_dim 128, scale 1/sqrt(128), fp16 storage, fp32 accumulation.
@@ -37,7 +38,7 @@
 extern "C" {
 #endif
 
-#define QATTN_ABI_VERSION 2
+#define QATTN_ABI_VERSION 3
 
 #define QATTN_Q_HEADS 16
 #define QATTN_KV_HEADS 8
@@ -190,6 +191,18 @@ int qattn_plan_mask(int32_t L, int32_t mask, int32_t prefix, int32_t window, uin
 int qattn_qk_norm_rope(qattn_ctx* ctx, void* x, int64_t row_stride, int64_t col0, int32_t heads,
                        const int32_t* cu_seqlens, int32_t nseq, const float* weight, double eps,
                        double theta, qattn_stream_t stream);
+
+/* ---- consumer: last-token pool + L2 norm  (replaces LastTokenPoolKernel, ops.ts:347-379) --- */
+/* For each sequence i < nseq: out[i*out_row_stride + d] = f32(x[r*row_stride + d]) * s for
+ * d < width, r = cu_seqlens[i+1]-1 (the reference's row b*S + lengths[b]-1 of its padded layout,
+ * ops.ts:357) and s = 1/sqrt(sum over d of f32(x)^2) (ops.ts:358-363).  As in the reference there
+ * is no epsilon: an all-zero row gives NaN.  An empty sequence (no last token; the reference
+ * never forms one) gets a row of zeros.  x: fp16 device rows, out: f32 device rows, both 16-byte
+ * aligned; width and row_stride multiples of 8 elements, out_row_stride >= width and a multiple
+ * of 4.  Enqueued on `stream` (NULL: the context stream); allocates nothing. */
+int qattn_pool_last_l2(qattn_ctx* ctx, const void* x, int64_t row_stride, int32_t width,
+                       const int32_t* cu_seqlens, int32_t nseq, float* out, int64_t out_row_stride,
+                       qattn_stream_t stream);
 
 /* ---- synthetic inputs ---------------------------------------------------------------------- */
 /* Element (r, c), r < rows, c < row_elems, at dst[r*row_stride + c] receives

@@ -7,6 +7,7 @@ Reference behaviour restated (paths relative to the reference checkout):
   src/webgpu/ops.ts:168-241   tiled flash attention (f16-faithful restatement: tiled16)
   src/webgpu/ops.ts:205-220   causal + 176-prefix/432-window mask
   src/webgpu/ops.ts:104-150   QK RMSNorm + RoPE producer, model.ts:76-83 RoPE table
+  src/webgpu/ops.ts:347-379   last-token pool + L2 normalisation (pool_last_l2)
 """
 import ctypes
 import os
@@ -129,6 +130,27 @@ def qk_norm_rope(x, cu_seqlens, heads, col0=0, weight=None, eps=1e-6, theta=1e6)
     lib().orc_qk_norm_rope(_ptr(x), x.shape[1], col0, heads, _ptr(cu), len(cu) - 1,
                            None if w is None else _ptr(w), eps, theta)
     return x
+
+
+def pool_last_l2(x, cu_seqlens, width=None):
+    """Last-token pool + L2 norm (LastTokenPoolKernel, src/webgpu/ops.ts:347-379), exact in f64.
+
+    x: fp16 rows [T, >= width]; sequence i pools row cu_seqlens[i+1]-1 (the reference's row
+    b*S + lengths[b]-1 of its padded layout, ops.ts:357): out = x / sqrt(sum x^2) over the first
+    `width` columns (ops.ts:358-363), as f64.  No epsilon, as in the reference: an all-zero row
+    gives NaN (0 * inverseSqrt(0)).  An empty sequence (which the reference never forms) gives
+    zeros, the library's documented choice."""
+    x = np.asarray(x)
+    width = x.shape[1] if width is None else width
+    cu = np.asarray(cu_seqlens, dtype=np.int64)
+    out = np.zeros((len(cu) - 1, width), dtype=np.float64)
+    for i in range(len(cu) - 1):
+        if cu[i + 1] == cu[i]:
+            continue
+        row = x[cu[i + 1] - 1, :width].astype(np.float64)
+        with np.errstate(divide="ignore", invalid="ignore"):
+            out[i] = row * (1.0 / np.sqrt(np.sum(row * row)))
+    return out
 
 
 def gen_lengths(seed_value, n, lo=10, hi=150):

@@ -50,6 +50,8 @@ hipError_t launch_fill_normal(half_t* dst, int64_t rows, int64_t row_elems, int6
                               uint64_t seed, hipStream_t stream);
 hipError_t launch_fill_token_rows(half_t* dst, const int32_t* ids, int64_t rows, int64_t row_elems,
                                   int64_t row_stride, uint64_t seed, hipStream_t stream);
+hipError_t launch_pool_last_l2(const half_t* x, int64_t row_stride, int width, const int32_t* cu_seqlens,
+                               int nseq, float* out, int64_t out_row_stride, hipStream_t stream);
 hipError_t launch_qk_norm_rope(half_t* x, int64_t row_stride, int64_t col0, int heads,
                                const int32_t* cu_dev, int nseq, int64_t T, const float* weight,
                                double eps, const float* rope_cos, const float* rope_sin,
@@ -899,6 +901,27 @@ int qattn_qk_norm_rope(qattn_ctx* ctx, void* x, int64_t row_stride, int64_t col0
   (void)hipFree(tab_dev);
   if (cu_dev) (void)hipFree(cu_dev);
   if (e != hipSuccess) return fail(ctx, QATTN_EHIP, "qk_norm_rope: %s", hipGetErrorString(e));
+  return QATTN_OK;
+}
+
+// ---- consumer: last-token pool + L2 normalisation ----------------------------------------------
+
+int qattn_pool_last_l2(qattn_ctx* ctx, const void* x, int64_t row_stride, int32_t width,
+                       const int32_t* cu_seqlens, int32_t nseq, float* out, int64_t out_row_stride,
+                       qattn_stream_t stream) {
+  if (!ctx || !x || !out) return fail(ctx, QATTN_EINVAL, "ctx/x/out is NULL");
+  if (width < 8 || width % 8 || row_stride < width || row_stride % 8)
+    return fail(ctx, QATTN_EINVAL, "width/row_stride (%d, %lld): width >= 8, both multiples of 8 elements, "
+                "row_stride >= width", width, (long long)row_stride);
+  if (out_row_stride < width || out_row_stride % 4)
+    return fail(ctx, QATTN_EINVAL, "out_row_stride %lld: >= width and a multiple of 4", (long long)out_row_stride);
+  if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(out) % 16)
+    return fail(ctx, QATTN_EINVAL, "x/out not 16-byte aligned");
+  int rc = validate_cu(ctx, cu_seqlens, nseq);
+  if (rc) return rc;
+  DeviceGuard g(ctx->device);
+  HIP_TRY(ctx, launch_pool_last_l2(static_cast<const half_t*>(x), row_stride, width, cu_seqlens, nseq, out,
+                                   out_row_stride, pick_stream(ctx, stream)));
   return QATTN_OK;
 }
 

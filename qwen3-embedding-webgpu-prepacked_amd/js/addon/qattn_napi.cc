@@ -564,6 +564,34 @@ napi_value QkNormRope(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
+// poolLastL2(ctx, x, rowStride, width, cuSeqlens, out): out (f32 rows of `width`) receives the
+// L2-normalised last row of each sequence of x (fp16 rows of rowStride elements).
+napi_value PoolLastL2(napi_env env, napi_callback_info info) {
+  napi_value argv[6];
+  if (!args_of(env, info, 6, argv)) return nullptr;
+  Ctx* c = live_ctx(env, argv[0]);
+  if (!c) return nullptr;
+  Buf* x = live_buf(env, argv[1]);
+  if (!x) return nullptr;
+  Buf* out = live_buf(env, argv[5]);
+  if (!out) return nullptr;
+  int64_t stride, width;
+  std::vector<int32_t> cu;
+  if (!get_i64(env, argv[2], &stride) || !get_i64(env, argv[3], &width) || !get_i32_array(env, argv[4], &cu) ||
+      cu.size() < 2 || width < 1 || width > INT32_MAX) {
+    napi_throw_type_error(env, nullptr, "expected (ctx, x, rowStride, width, cuSeqlens, out)");
+    return nullptr;
+  }
+  if ((size_t)cu.back() * (size_t)stride * 2 > x->bytes || (cu.size() - 1) * (size_t)width * 4 > out->bytes) {
+    napi_throw_range_error(env, nullptr, "rows exceed the buffers");
+    return nullptr;
+  }
+  int rc = qattn_pool_last_l2(c->ctx, x->ptr, stride, (int32_t)width, cu.data(), (int32_t)cu.size() - 1,
+                              static_cast<float*>(out->ptr), width, nullptr);
+  if (rc) return throw_qattn(env, rc, c->ctx);
+  return undefined(env);
+}
+
 napi_value Synchronize(napi_env env, napi_callback_info info) {
   napi_value argv[1];
   if (!args_of(env, info, 1, argv)) return nullptr;
@@ -636,6 +664,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"planDescribe", PlanDescribe}, {"planMask", PlanMask},
       {"debugMask", DebugMask},       {"genQkv", GenQkv},
       {"fillTokenRows", FillTokenRows}, {"qkNormRope", QkNormRope},
+      {"poolLastL2", PoolLastL2},
       {"synchronize", Synchronize},   {"synchronizeAsync", SynchronizeAsync},
   };
   for (const Fn& f : fns) {

@@ -58,6 +58,7 @@ class HipAttentionPlan {
     this.v = ctx.alloc(this.capacity * 1024 * 2);
     this.o = ctx.alloc(this.capacity * 2048 * 2);
     this.last = ctx.alloc(batch * 2048 * 2);
+    this.embeddings = ctx.alloc(batch * 2048 * 4);
   }
 
   async run(ids, lengths) {
@@ -84,18 +85,22 @@ class HipAttentionPlan {
         addon.qkNormRope(ctx.handle, this.k.handle, 1024, 0, 8, cu, 1e-6, 1e6);
         rt.attention.encode(run);
       }
+      // Last-token pool + L2 norm on the device (LastTokenPoolKernel, ops.ts:347-379) over the
+      // o_last rows, one per request.
+      addon.poolLastL2(ctx.handle, this.last.handle, 2048, 2048, Int32Array.from({ length: this.batch + 1 }, (_, i) => i),
+        this.embeddings.handle);
       await ctx.synchronizeAsync();
     } finally {
       rt.attention.destroyRun(run);
     }
-    const bits = this.last.read(new Uint16Array(this.batch * 2048));
+    const flat = this.embeddings.read(new Float32Array(this.batch * 2048));
     const out = [];
-    for (let i = 0; i < this.batch; i += 1) out.push(l2Normalize(halvesToFloat32(bits.subarray(i * 2048, (i + 1) * 2048))));
+    for (let i = 0; i < this.batch; i += 1) out.push(flat.slice(i * 2048, (i + 1) * 2048));
     return out;
   }
 
   destroy() {
-    for (const b of [this.ids, this.q, this.k, this.v, this.o, this.last]) b.destroy();
+    for (const b of [this.ids, this.q, this.k, this.v, this.o, this.last, this.embeddings]) b.destroy();
   }
 }
 

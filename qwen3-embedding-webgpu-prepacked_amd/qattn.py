@@ -97,6 +97,7 @@ def lib():
         "qattn_plan_mask": (ctypes.c_int, [i32, i32, i32, i32, vp]),
         "qattn_qk_norm_rope": (ctypes.c_int, [vp, vp, i64, i64, i32, vp, i32, vp,
                                               ctypes.c_double, ctypes.c_double, vp]),
+        "qattn_pool_last_l2": (ctypes.c_int, [vp, vp, i64, i32, vp, i32, vp, i64, vp]),
         "qattn_fill_normal": (ctypes.c_int, [vp, vp, i64, i64, i64, ctypes.c_uint64, vp]),
         "qattn_fill_token_rows": (ctypes.c_int, [vp, vp, vp, i64, i64, i64, ctypes.c_uint64, vp]),
         "qattn_gen_qkv": (ctypes.c_int, [vp, ctypes.c_uint32, ctypes.c_uint32, vp, i32,
@@ -307,6 +308,15 @@ class Context:
         cu = np.ascontiguousarray(cu_seqlens, dtype=np.int32)
         _check(lib().qattn_qk_norm_rope(self.handle, x_ptr, row_stride, col0, heads, _np_ptr(cu),
                                         len(cu) - 1, weight_ptr, eps, theta, stream), self.handle)
+
+    def pool_last_l2(self, x_ptr, row_stride, width, cu_seqlens, out_ptr, out_row_stride=None,
+                     stream=None):
+        """Last row of each sequence, L2-normalised, fp16 -> f32 (LastTokenPoolKernel,
+        ops.ts:347-379)."""
+        cu = np.ascontiguousarray(cu_seqlens, dtype=np.int32)
+        _check(lib().qattn_pool_last_l2(self.handle, x_ptr, row_stride, width, _np_ptr(cu), len(cu) - 1,
+                                        out_ptr, width if out_row_stride is None else out_row_stride,
+                                        stream), self.handle)
 
     def fill_normal(self, ptr, rows, row_elems, row_stride, seed, stream=None):
         _check(lib().qattn_fill_normal(self.handle, ptr, rows, row_elems, row_stride, seed, stream),

@@ -6,6 +6,7 @@ const fs = require('fs');
 const path = require('path');
 const pkg = require(path.join(__dirname, '..', '..', 'qwen3-embedding-webgpu-prepacked_amd', 'js'));
 const { Qwen3EmbeddingEngine, HipAttentionRuntime, DeviceContext, CausalAttentionKernel } = pkg;
+const { halvesToFloat32, l2Normalize } = require(path.join(__dirname, '..', '..', 'qwen3-embedding-webgpu-prepacked_amd', 'js', 'runtime.js'));
 
 const work = process.argv[2];
 const cases = [];
@@ -103,6 +104,23 @@ test('engine.embed() end to end: unit vectors; a request alone equals the same r
   let dot = 0;
   for (let d = 0; d < 2048; d += 1) dot += a[d] * b[d];
   assert.ok(dot < 0.999, 'different token ids give different outputs');
+  for (const p of runtime.plans) p.destroy();
+  runtime.plans = [];
+});
+
+test('device pool (poolLastL2) equals the host L2 normalisation of the o_last rows', async () => {
+  const runtime = new HipAttentionRuntime({ context: ctx, layers: 2 });
+  const plan = runtime.createPlan(3, 40);
+  const lengths = [40, 1, 17];
+  const ids = Array.from({ length: 58 }, (_, i) => (i * 7919) % 151000);
+  const got = await plan.run(ids, lengths);
+  const bits = plan.last.read(new Uint16Array(3 * 2048));
+  for (let i = 0; i < 3; i += 1) {
+    const want = l2Normalize(halvesToFloat32(bits.subarray(i * 2048, (i + 1) * 2048)));
+    for (let d = 0; d < 2048; d += 1) {
+      assert.ok(Math.abs(got[i][d] - want[d]) <= 3e-6 * Math.abs(want[d]) + 1e-12, `row ${i} dim ${d}: ${got[i][d]} vs ${want[d]}`);
+    }
+  }
   for (const p of runtime.plans) p.destroy();
   runtime.plans = [];
 });

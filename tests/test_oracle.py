@@ -352,3 +352,54 @@ def test_tiled16_varlen_equals_padded_reference_layout(oracle):
     # In the padded layout sequence 0 sees its padding rows as keys > q (masked) -- same result.
     assert np.array_equal(padded[:20], packed[:20])
     assert np.array_equal(padded[S:], packed[20:])
+
+
+# ---- last-token pool + L2 norm (ops.ts:347-379) -------------------------------------------------
+
+def test_pool_closed_forms(oracle):
+    # A row of 3, 4, zeros -> 0.6, 0.8, zeros; a constant row c of width W -> sign(c)/sqrt(W).
+    x = np.zeros((3, 1024), np.float16)
+    x[0, :2] = [3, 4]
+    x[1, :] = -0.5
+    x[2, :] = 2.0
+    out = oracle.pool_last_l2(x, [0, 1, 2, 3])
+    assert np.allclose(out[0, :2], [0.6, 0.8], rtol=0, atol=1e-15) and not out[0, 2:].any()
+    assert np.allclose(out[1], -1 / math.sqrt(1024), rtol=0, atol=1e-15)
+    assert np.allclose(out[2], 1 / math.sqrt(1024), rtol=0, atol=1e-15)
+
+
+def test_pool_reads_the_last_row_of_each_sequence(oracle):
+    # Rows differ in where their mass is, so pooling any other row (the first, or the next
+    # sequence's) gives a different unit vector.
+    lengths = [1, 4, 2, 7]
+    cu = np.concatenate([[0], np.cumsum(lengths)])
+    x = np.zeros((cu[-1], 64), np.float16)
+    for t in range(cu[-1]):
+        x[t, t % 64] = 1.0 + t
+    out = oracle.pool_last_l2(x, cu)
+    for i in range(len(lengths)):
+        last = cu[i + 1] - 1
+        want = np.zeros(64)
+        want[last % 64] = 1.0
+        assert np.array_equal(out[i], want)
+
+
+def test_pool_unit_norm_and_scale_invariance(oracle):
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((40, 2048)).astype(np.float16)
+    cu = [0, 9, 9, 25, 40]  # includes an empty sequence
+    out = oracle.pool_last_l2(x, cu)
+    norms = np.sqrt(np.sum(out * out, axis=1))
+    assert np.allclose(norms[[0, 2, 3]], 1.0, rtol=0, atol=1e-12)
+    assert not out[1].any()  # empty sequence: zeros
+    # scaling a row by a power of two is exact in fp16 and leaves the unit vector unchanged
+    assert np.array_equal(oracle.pool_last_l2(x * np.float16(8), cu), out)
+    # width restricts the columns
+    part = oracle.pool_last_l2(x, cu, width=1024)
+    assert np.allclose(np.sqrt(np.sum(part[[0, 2, 3]] ** 2, axis=1)), 1.0, atol=1e-12)
+
+
+def test_pool_zero_row_gives_nan_as_the_reference(oracle):
+    # inverseSqrt(0) is +inf in the reference and 0 * inf = NaN: no epsilon (ops.ts:362-363).
+    out = oracle.pool_last_l2(np.zeros((2, 16), np.float16), [0, 2])
+    assert np.isnan(out).all()
