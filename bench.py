@@ -184,6 +184,45 @@ def pool_timing(reps):
     ctx.close()
 
 
+def q4_timing(reps):
+    """The projection kernel alone (not the headline metric): qattn_q4_matmul at the shapes one
+    layer of the 16 x 500 packing multiplies (M = 8000 tokens): the fused QKV projection
+    (K 1024 -> N 4096), the attention output projection (2048 -> 1024), the gate/up projection
+    (1024 -> 6144) and the down projection (3072 -> 1024).  Random Q4_0 records, `reps` launches
+    per shape between HIP events; algorithmic FLOP = 2 M N K.  One JSON line per shape."""
+    q = load_binding()
+    ctx = q.Context(0)
+    rng = np.random.default_rng(0)
+    M = 8000
+    for name, K, N in (("qkv", 1024, 4096), ("attn_out", 2048, 1024), ("gate_up", 1024, 6144), ("down", 3072, 1024)):
+        nbytes = q.lib().qattn_q4_compact_bytes(K, N)
+        wts = rng.integers(0, 256, size=nbytes, dtype=np.uint8)
+        rec = wts.reshape(-1, 20)
+        rec[:, 0:2] = np.full((rec.shape[0], 1), 0.01, np.float16).view(np.uint8)  # scale 0.01
+        bw = ctx.upload(wts)
+        bx, by = ctx.alloc(M * K * 2), ctx.alloc(M * N * 2)
+        ctx.fill_normal(bx.ptr, M, K, K, 11)
+        for _ in range(3):
+            ctx.q4_matmul(bx.ptr, M, K, bw.ptr, nbytes, N, by.ptr)
+        e0, e1 = ctx.event(), ctx.event()
+        ctx.synchronize()
+        e0.record()
+        for _ in range(reps):
+            ctx.q4_matmul(bx.ptr, M, K, bw.ptr, nbytes, N, by.ptr)
+        e1.record()
+        ctx.synchronize()
+        us = e0.elapsed_ms(e1) * 1000.0 / reps
+        flop = 2.0 * M * N * K
+        print(json.dumps({"kernel": "q4_matmul_kernel", "shape": name, "M": M, "K": K, "N": N, "launches": reps,
+                          "us_per_launch": round(us, 2), "TFLOP/s": round(flop / us / 1e6, 1),
+                          "frac_of_fp16_peak": round(flop / us / 1e6 / PEAK_FP16_TFLOPS, 3)}), flush=True)
+        for b in (bw, bx, by):
+            b.free()
+        e0.destroy()
+        e1.destroy()
+    ctx.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -196,7 +235,12 @@ def main():
                          "known-size reference for rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
     ap.add_argument("--pool", type=int, default=0, metavar="N",
                     help="only time N launches of the last-token pool kernel per width and exit")
+    ap.add_argument("--q4", type=int, default=0, metavar="N",
+                    help="only time N launches of the Q4_0 dequant-GEMM per projection shape and exit")
     args = ap.parse_args()
+    if args.q4:
+        q4_timing(args.q4)
+        return
     if args.pool:
         pool_timing(args.pool)
         return

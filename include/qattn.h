@@ -17,6 +17,7 @@
  *   RoPE table                         model.ts:76-83   | built inside qattn_qk_norm_rope
  *   last-token row of poolShader       ops.ts:357       | qattn_run_desc.o_last
  *   LastTokenPoolKernel (L2 norm)      ops.ts:347-379   | qattn_pool_last_l2
+ *   compact Q4_0 batch matmul   quant-matmul.ts:267-307 | qattn_q4_matmul
  *
  * Fixed model geometry (model.ts:18-23, ops.ts:196): 16 query heads, 8 KV heads (query head h
  * reads KV head h/2), head_dim 128, scale 1/sqrt(128), fp16 storage, fp32 accumulation.
@@ -191,6 +192,22 @@ int qattn_plan_mask(int32_t L, int32_t mask, int32_t prefix, int32_t window, uin
 int qattn_qk_norm_rope(qattn_ctx* ctx, void* x, int64_t row_stride, int64_t col0, int32_t heads,
                        const int32_t* cu_seqlens, int32_t nseq, const float* weight, double eps,
                        double theta, qattn_stream_t stream);
+
+/* ---- projection: Q4_0 tile32-compact dequant-GEMM  (replaces the compact batch matmul, ------ */
+/* ---- quant-matmul.ts:267-307, over the layout of packQ40Tile32, prepacked/format.ts:64-96) -- */
+/* Bytes of an N x K weight tensor in the q4_0-tile32-compact layout: ceil(N/32) tiles of K/32
+ * blocks of 32 records of 20 bytes (-1 if K is not a positive multiple of 32 or N < 1). */
+int64_t qattn_q4_compact_bytes(int32_t K, int32_t N);
+/* y[m*ldy + n] = f16(sum over k < K of x[m*ldx + k] * W(n, k)) for m < M, n < N, where
+ * W(n, k) = f16(scale * (q - 8)) from record ((n/32)*(K/32) + k/32)*32 + n%32 of `w`: the f16
+ * scale in bytes 0-1, element j of the 32-column block in the low nibble of byte 4+j, element
+ * j+16 in its high nibble (the reference's dequant, quant-matmul.ts:99-108).  Products and sums
+ * in fp32 (the reference accumulates in f16).  x, y: fp16 device rows, 16-byte aligned, ldx >= K
+ * and ldy >= N multiples of 8 elements; w: device, 4-byte aligned, w_bytes >=
+ * qattn_q4_compact_bytes(K, N).  Enqueued on `stream` (NULL: the context stream); allocates
+ * nothing. */
+int qattn_q4_matmul(qattn_ctx* ctx, const void* x, int64_t ldx, int32_t M, int32_t K, const void* w,
+                    int64_t w_bytes, int32_t N, void* y, int64_t ldy, qattn_stream_t stream);
 
 /* ---- consumer: last-token pool + L2 norm  (replaces LastTokenPoolKernel, ops.ts:347-379) --- */
 /* For each sequence i < nseq: out[i*out_row_stride + d] = f32(x[r*row_stride + d]) * s for

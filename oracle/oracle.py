@@ -8,6 +8,9 @@ Reference behaviour restated (paths relative to the reference checkout):
   src/webgpu/ops.ts:205-220   causal + 176-prefix/432-window mask
   src/webgpu/ops.ts:104-150   QK RMSNorm + RoPE producer, model.ts:76-83 RoPE table
   src/webgpu/ops.ts:347-379   last-token pool + L2 normalisation (pool_last_l2)
+  src/prepacked/format.ts:64-96, src/webgpu/quant-matmul.ts:99-108, 267-307
+                              Q4_0 tile32-compact packing and the dequant-GEMM (pack_q40_tile32,
+                              q40_compact_weights, q4_matmul)
 """
 import ctypes
 import os
@@ -151,6 +154,55 @@ def pool_last_l2(x, cu_seqlens, width=None):
         with np.errstate(divide="ignore", invalid="ignore"):
             out[i] = row * (1.0 / np.sqrt(np.sum(row * row)))
     return out
+
+
+def pack_q40_tile32(parts):
+    """packQ40Tile32 (src/prepacked/format.ts:64-96): GGML Q4_0 rows (18-byte blocks: f16 scale,
+    16 quant bytes; element j of a block in the low nibble of byte j, element j+16 in its high
+    nibble) of one or more parts (k, n, bytes), stacked by rows, into 20-byte records (scale,
+    2 zero bytes, the 16 quant bytes) ordered ((n // 32) * (k // 32) + k_block) * 32 + n % 32.
+    Rows past n in the last 32-row tile stay zero.  Returns (bytes as uint8, k, n)."""
+    k = parts[0][0]
+    if k % 32:
+        raise ValueError(f"K={k} is not divisible by 32")
+    rows = []
+    for pk, pn, pbytes in parts:
+        if pk != k:
+            raise ValueError("mismatched K dimensions")
+        pbytes = np.frombuffer(bytes(pbytes), np.uint8)
+        if pbytes.size != pn * (k // 32) * 18:
+            raise ValueError("part size")
+        rows.append(pbytes.reshape(pn, k // 32, 18))
+    src = np.concatenate(rows, axis=0)
+    n, kb = src.shape[0], k // 32
+    tiles = -(-n // 32)
+    out = np.zeros((tiles, kb, 32, 20), np.uint8)
+    for r in range(n):
+        out[r // 32, :, r % 32, 0:2] = src[r, :, 0:2]
+        out[r // 32, :, r % 32, 4:20] = src[r, :, 2:18]
+    return out.reshape(-1), k, n
+
+
+def q40_compact_weights(packed, k, n):
+    """The fp16 weights W[n, k] a tile32-compact tensor holds, as the reference's compact shaders
+    dequantise them (quant-matmul.ts:99-108, 276-282): f16(scale) * (q - 8), rounded to f16 (the
+    f32 product is exact, so this equals the shader's f16 multiply)."""
+    kb = k // 32
+    rec = np.asarray(packed, np.uint8).reshape(-1, kb, 32, 20)
+    scale = rec[..., 0:2].copy().view(np.float16)[..., 0].astype(np.float32)    # [tiles, kb, 32]
+    q = rec[..., 4:20]
+    lo = (q & 15).astype(np.float32) - 8.0
+    hi = (q >> 4).astype(np.float32) - 8.0
+    vals = np.concatenate([lo, hi], axis=-1) * scale[..., None]                   # [tiles, kb, 32, 32]
+    w = vals.transpose(0, 2, 1, 3).reshape(-1, k)                                 # rows tile*32 + r
+    return w[:n].astype(np.float16)
+
+
+def q4_matmul(x, packed, k, n):
+    """Y = X W^T exactly (f64) for fp16 X [m, k] and the tile32-compact weights W [n, k]: the
+    compact batch matmul's result (quant-matmul.ts:267-307) without its f16 accumulation."""
+    w = q40_compact_weights(packed, k, n).astype(np.float64)
+    return np.asarray(x, np.float16).astype(np.float64) @ w.T
 
 
 def gen_lengths(seed_value, n, lo=10, hi=150):

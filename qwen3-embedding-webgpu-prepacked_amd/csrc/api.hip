@@ -50,6 +50,8 @@ hipError_t launch_fill_normal(half_t* dst, int64_t rows, int64_t row_elems, int6
                               uint64_t seed, hipStream_t stream);
 hipError_t launch_fill_token_rows(half_t* dst, const int32_t* ids, int64_t rows, int64_t row_elems,
                                   int64_t row_stride, uint64_t seed, hipStream_t stream);
+hipError_t launch_q4_matmul(const half_t* x, int64_t ldx, int M, int K, const uint8_t* w, uint32_t w_bytes, int N,
+                            half_t* y, int64_t ldy, hipStream_t stream);
 hipError_t launch_pool_last_l2(const half_t* x, int64_t row_stride, int width, const int32_t* cu_seqlens,
                                int nseq, float* out, int64_t out_row_stride, hipStream_t stream);
 hipError_t launch_qk_norm_rope(half_t* x, int64_t row_stride, int64_t col0, int heads,
@@ -901,6 +903,35 @@ int qattn_qk_norm_rope(qattn_ctx* ctx, void* x, int64_t row_stride, int64_t col0
   (void)hipFree(tab_dev);
   if (cu_dev) (void)hipFree(cu_dev);
   if (e != hipSuccess) return fail(ctx, QATTN_EHIP, "qk_norm_rope: %s", hipGetErrorString(e));
+  return QATTN_OK;
+}
+
+// ---- projection: Q4_0 tile32-compact dequant-GEMM -------------------------------------------------
+
+int64_t qattn_q4_compact_bytes(int32_t K, int32_t N) {
+  if (K < 32 || K % 32 || N < 1) return -1;
+  return (int64_t)((N + 31) / 32) * (K / 32) * 32 * 20;
+}
+
+int qattn_q4_matmul(qattn_ctx* ctx, const void* x, int64_t ldx, int32_t M, int32_t K, const void* w,
+                    int64_t w_bytes, int32_t N, void* y, int64_t ldy, qattn_stream_t stream) {
+  if (!ctx || !x || !w || !y) return fail(ctx, QATTN_EINVAL, "ctx/x/w/y is NULL");
+  if (M < 0 || N < 1 || K < 32 || K % 32)
+    return fail(ctx, QATTN_EINVAL, "shape M=%d K=%d N=%d: M >= 0, N >= 1, K a positive multiple of 32", M, K, N);
+  if (ldx < K || ldx % 8 || ldy < N || ldy % 8)
+    return fail(ctx, QATTN_EINVAL, "ldx/ldy (%lld, %lld): >= K / N and multiples of 8 elements", (long long)ldx,
+                (long long)ldy);
+  const int64_t need = qattn_q4_compact_bytes(K, N);
+  if (w_bytes < need || w_bytes > 0x7FFFFFFFll)
+    return fail(ctx, QATTN_EINVAL, "w_bytes %lld: a %dx%d tile32-compact tensor holds %lld bytes (< 2 GiB)",
+                (long long)w_bytes, N, K, (long long)need);
+  if (((int64_t)M + 128) * ldx * 2 > 0x7FFFFFFFll || (int64_t)M * ldy * 2 > 0x7FFFFFFFll)
+    return fail(ctx, QATTN_EINVAL, "x or y rows beyond 2 GiB (32-bit buffer offsets)");
+  if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(y) % 16 || reinterpret_cast<uintptr_t>(w) % 4)
+    return fail(ctx, QATTN_EINVAL, "x/y not 16-byte or w not 4-byte aligned");
+  DeviceGuard g(ctx->device);
+  HIP_TRY(ctx, launch_q4_matmul(static_cast<const half_t*>(x), ldx, M, K, static_cast<const uint8_t*>(w),
+                                (uint32_t)w_bytes, N, static_cast<half_t*>(y), ldy, pick_stream(ctx, stream)));
   return QATTN_OK;
 }
 

@@ -98,6 +98,8 @@ def lib():
         "qattn_qk_norm_rope": (ctypes.c_int, [vp, vp, i64, i64, i32, vp, i32, vp,
                                               ctypes.c_double, ctypes.c_double, vp]),
         "qattn_pool_last_l2": (ctypes.c_int, [vp, vp, i64, i32, vp, i32, vp, i64, vp]),
+        "qattn_q4_compact_bytes": (i64, [i32, i32]),
+        "qattn_q4_matmul": (ctypes.c_int, [vp, vp, i64, i32, i32, vp, i64, i32, vp, i64, vp]),
         "qattn_fill_normal": (ctypes.c_int, [vp, vp, i64, i64, i64, ctypes.c_uint64, vp]),
         "qattn_fill_token_rows": (ctypes.c_int, [vp, vp, vp, i64, i64, i64, ctypes.c_uint64, vp]),
         "qattn_gen_qkv": (ctypes.c_int, [vp, ctypes.c_uint32, ctypes.c_uint32, vp, i32,
@@ -317,6 +319,11 @@ class Context:
         _check(lib().qattn_pool_last_l2(self.handle, x_ptr, row_stride, width, _np_ptr(cu), len(cu) - 1,
                                         out_ptr, width if out_row_stride is None else out_row_stride,
                                         stream), self.handle)
+
+    def q4_matmul(self, x_ptr, M, K, w_ptr, w_bytes, N, y_ptr, ldx=None, ldy=None, stream=None):
+        """y = x W^T for tile32-compact Q4_0 weights W [N, K] (quant-matmul.ts:267-307)."""
+        _check(lib().qattn_q4_matmul(self.handle, x_ptr, K if ldx is None else ldx, M, K, w_ptr, w_bytes, N,
+                                     y_ptr, N if ldy is None else ldy, stream), self.handle)
 
     def fill_normal(self, ptr, rows, row_elems, row_stride, seed, stream=None):
         _check(lib().qattn_fill_normal(self.handle, ptr, rows, row_elems, row_stride, seed, stream),

@@ -238,3 +238,14 @@ def test_kernel_key_iteration_matches_reference_mask(qattn, oracle, L):
                                          (333, 1, 1, 200), (1000, 1, 300, 64)])
 def test_kernel_key_iteration_other_masks(qattn, oracle, L, mask, P, W):
     assert np.array_equal(qattn.plan_mask(L, mask, P, W), oracle.mask_bits(L, mask, P, W))
+
+
+def test_q4_compact_bytes(qattn, oracle):
+    f = qattn.lib().qattn_q4_compact_bytes
+    assert f(1024, 4096) == 128 * 32 * 32 * 20
+    assert f(96, 70) == 3 * 3 * 32 * 20
+    assert f(32, 1) == 32 * 20
+    assert f(33, 1) == -1 and f(0, 5) == -1 and f(64, 0) == -1
+    # the oracle's packer writes exactly that many bytes
+    packed, k, n = oracle.pack_q40_tile32([(96, 70, bytes(70 * 3 * 18))])
+    assert packed.size == f(96, 70)

@@ -1,0 +1,104 @@
+"""GPU parity of the Q4_0 tile32-compact dequant-GEMM (qattn_q4_matmul, replacing the reference's
+compact batch matmul, src/webgpu/quant-matmul.ts:267-307) against the f64 oracle, through the C ABI.
+
+Tolerance, per element: the fp32 sum of K exact products (f16 x f16 products are exact in fp32)
+errs by at most (K + 2) u32 * sum_k |x_k w_k| (u32 = 2^-24), and the final fp16 rounding by half an
+ulp: |y - exact| <= 2^-11 |exact| + (K + 2) 2^-24 (|x| |w|^T) + 2^-25 (fp16 subnormal spacing).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def random_compact(rng, n, k, scale_lo=0.002, scale_hi=0.05):
+    """A tile32-compact tensor of random Q4_0 records; rows past n in the last tile stay zero."""
+    tiles, kb = -(-n // 32), k // 32
+    rec = np.zeros((tiles, kb, 32, 20), np.uint8)
+    scales = rng.uniform(scale_lo, scale_hi, size=(tiles, kb, 32)).astype(np.float16)
+    scales *= np.where(rng.random(scales.shape) < 0.5, -1, 1).astype(np.float16)
+    rec[..., 0:2] = scales.view(np.uint8).reshape(tiles, kb, 32, 2)
+    rec[..., 4:20] = rng.integers(0, 256, size=(tiles, kb, 32, 16), dtype=np.uint8)
+    flat = rec.reshape(-1, 20)
+    rows = (np.arange(tiles)[:, None, None] * 32 + np.arange(32)[None, None, :]).repeat(kb, axis=1).reshape(-1)
+    flat[rows >= n] = 0
+    return flat.reshape(-1)
+
+
+def run_q4(ctx, x, packed, k, n, ldx=None, ldy=None):
+    m = x.shape[0]
+    ldx = k if ldx is None else ldx
+    ldy = -(-n // 8) * 8 if ldy is None else ldy
+    xs = np.zeros((max(m, 1), ldx), np.float16)
+    xs[:m, :k] = x
+    bx, bw = ctx.upload(xs.view(np.uint16)), ctx.upload(packed)
+    by = ctx.alloc(max(m, 1) * ldy * 2)
+    by.fill_u16(0x7E00)  # NaN: every valid element must be written
+    ctx.q4_matmul(bx.ptr, m, k, bw.ptr, packed.size, n, by.ptr, ldx=ldx, ldy=ldy)
+    ctx.synchronize()
+    y = by.read(np.uint16, (max(m, 1), ldy)).view(np.float16)
+    for b in (bx, bw, by):
+        b.free()
+    return y[:m]
+
+
+def check(oracle, y, x, packed, k, n, label):
+    exact = oracle.q4_matmul(x, packed, k, n)
+    w = oracle.q40_compact_weights(packed, k, n).astype(np.float64)
+    mag = np.abs(x.astype(np.float64)) @ np.abs(w).T
+    bound = 2.0 ** -11 * np.abs(exact) + (k + 2) * 2.0 ** -24 * mag + 2.0 ** -25
+    got = y[:, :n].astype(np.float64)
+    err = np.abs(got - exact)
+    print(f"[{label}] max|err| {err.max():.3e}  max err/bound {np.max(err / bound):.3f}", flush=True)
+    assert np.isfinite(got).all(), label
+    assert (err <= bound).all(), label
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 32, 1), (130, 96, 70), (64, 128, 128), (257, 2048, 1024),
+                                   (33, 3072, 1024), (1280, 1024, 4096)])
+def test_q4_matmul_matches_oracle(ctx, oracle, m, k, n):
+    rng = np.random.default_rng(m * 7 + k + n)
+    packed = random_compact(rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    y = run_q4(ctx, x, packed, k, n)
+    check(oracle, y, x, packed, k, n, f"q4 {m}x{k}x{n}")
+
+
+def test_q4_matmul_strides_and_untouched_padding(ctx, oracle):
+    rng = np.random.default_rng(1)
+    m, k, n = 70, 160, 40
+    packed = random_compact(rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    y = run_q4(ctx, x, packed, k, n, ldx=k + 24, ldy=n + 8)
+    check(oracle, y, x, packed, k, n, "q4 strided")
+    assert np.isnan(y[:, n:].astype(np.float32)).all()  # columns past N are not written
+
+
+def test_q4_matmul_reference_format_vector(ctx, oracle):
+    # The reference's packing test (tests/prepacked-format.test.ts:13-22) as weights: row 0 holds
+    # q - 8 (scale 1), row 1 holds 2 (7 - q) (scale 2); x = e_j picks column j.
+    def block(scale_bits, quants):
+        b = bytearray(18)
+        b[0:2] = bytes(scale_bits)
+        for i in range(16):
+            b[2 + i] = quants[i] | (quants[i + 16] << 4)
+        return bytes(b)
+    first = block([0x00, 0x3C], [i & 15 for i in range(32)])
+    second = block([0x00, 0x40], [15 - (i & 15) for i in range(32)])
+    packed, k, n = oracle.pack_q40_tile32([(32, 1, first), (32, 1, second)])
+    x = np.eye(32, dtype=np.float16)
+    y = run_q4(ctx, x, packed, k, n).astype(np.float64)
+    assert np.array_equal(y[:, 0], [(j & 15) - 8 for j in range(32)])
+    assert np.array_equal(y[:, 1], [2 * (7 - (j & 15)) for j in range(32)])
+
+
+def test_q4_matmul_invalid_arguments(ctx, qattn):
+    buf = ctx.alloc(1 << 16)
+    good = dict(m=4, k=64, n=8, w_bytes=qattn.lib().qattn_q4_compact_bytes(64, 8), ldx=64, ldy=8, x_off=0)
+    for bad in (dict(k=48), dict(w_bytes=100), dict(ldx=60), dict(ldy=12), dict(x_off=8), dict(n=0)):
+        a = dict(good, **bad)
+        with pytest.raises(qattn.QattnError) as e:
+            ctx.q4_matmul(buf.ptr + a["x_off"], a["m"], a["k"], buf.ptr, a["w_bytes"], a["n"], buf.ptr,
+                          ldx=a["ldx"], ldy=a["ldy"])
+        assert e.value.code == qattn.EINVAL, bad
+    buf.free()

@@ -403,3 +403,74 @@ def test_pool_zero_row_gives_nan_as_the_reference(oracle):
     # inverseSqrt(0) is +inf in the reference and 0 * inf = NaN: no epsilon (ops.ts:362-363).
     out = oracle.pool_last_l2(np.zeros((2, 16), np.float16), [0, 2])
     assert np.isnan(out).all()
+
+
+# ---- Q4_0 tile32-compact packing and dequant-GEMM (format.ts:64-96, quant-matmul.ts) ----------
+
+def _q40_block(scale_bits, quants):
+    b = bytearray(18)
+    b[0:2] = bytes(scale_bits)
+    for i in range(16):
+        b[2 + i] = quants[i] | (quants[i + 16] << 4)
+    return bytes(b)
+
+
+def test_pack_q40_tile32_reference_vector(oracle):
+    # The reference's own test (tests/prepacked-format.test.ts:13-22): two one-row parts.
+    first = _q40_block([0x00, 0x3C], [i & 15 for i in range(32)])
+    second = _q40_block([0x00, 0x40], [15 - (i & 15) for i in range(32)])
+    packed, k, n = oracle.pack_q40_tile32([(32, 1, first), (32, 1, second)])
+    assert (k, n) == (32, 2) and packed.size == 32 * 20
+    assert list(packed[0:8]) == [0x00, 0x3C, 0x00, 0x00, 0x00, 0x11, 0x22, 0x33]
+    assert list(packed[20:28]) == [0x00, 0x40, 0x00, 0x00, 0xFF, 0xEE, 0xDD, 0xCC]
+    assert not packed[40:].any()  # rows 2..31 of the tile are zero
+
+
+def test_q40_weights_closed_form(oracle):
+    # Scale 1.0 (0x3C00) and quants q -> q - 8; scale 2.0 (0x4000) and 15 - q -> 2 * (7 - q).
+    first = _q40_block([0x00, 0x3C], [i & 15 for i in range(32)])
+    second = _q40_block([0x00, 0x40], [15 - (i & 15) for i in range(32)])
+    packed, k, n = oracle.pack_q40_tile32([(32, 1, first), (32, 1, second)])
+    w = oracle.q40_compact_weights(packed, k, n).astype(np.float64)
+    assert np.array_equal(w[0], [(i & 15) - 8 for i in range(32)])
+    assert np.array_equal(w[1], [2 * (7 - (i & 15)) for i in range(32)])
+
+
+def test_q40_tile_order_across_tiles_and_k_blocks(oracle):
+    # 70 rows (3 tiles, the last partial) x 96 columns (3 K blocks): every (row, k block) gets its
+    # own scale, so a transposed tile / block / row index gives different weights.
+    rng = np.random.default_rng(5)
+    n, k = 70, 96
+    rows = []
+    for r in range(n):
+        for kb in range(k // 32):
+            scale = np.array([1 + r + 0.25 * kb], np.float16).view(np.uint8)
+            rows.append(_q40_block(list(scale), list(rng.integers(0, 16, 32))))
+    raw = b"".join(rows)
+    packed, _, _ = oracle.pack_q40_tile32([(k, 40, raw[:40 * 3 * 18]), (k, 30, raw[40 * 3 * 18:])])
+    assert packed.size == 3 * 3 * 32 * 20
+    w = oracle.q40_compact_weights(packed, k, n).astype(np.float64)
+    src = np.frombuffer(raw, np.uint8).reshape(n, 3, 18)
+    for r in (0, 31, 32, 45, 69):
+        for kb in range(3):
+            scale = float(src[r, kb, 0:2].copy().view(np.float16)[0])
+            q = src[r, kb, 2:18]
+            want = np.concatenate([(q & 15), (q >> 4)]).astype(np.float64) - 8
+            assert np.array_equal(w[r, 32 * kb:32 * kb + 32], np.float16(want * scale).astype(np.float64))
+
+
+def test_q4_matmul_against_dense_product(oracle):
+    rng = np.random.default_rng(9)
+    m, k, n = 5, 64, 33
+    blocks = []
+    for r in range(n):
+        for kb in range(2):
+            blocks.append(_q40_block(list(np.array([rng.uniform(0.01, 0.1)], np.float16).view(np.uint8)),
+                                     list(rng.integers(0, 16, 32))))
+    packed, _, _ = oracle.pack_q40_tile32([(k, n, b"".join(blocks))])
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    w = oracle.q40_compact_weights(packed, k, n).astype(np.float64)
+    y = oracle.q4_matmul(x, packed, k, n)
+    for i in range(m):
+        for j in range(n):
+            assert abs(y[i, j] - sum(float(x[i, c]) * w[j, c] for c in range(k))) < 1e-12
