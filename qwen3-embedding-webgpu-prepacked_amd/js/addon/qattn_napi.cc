@@ -564,6 +564,34 @@ napi_value QkNormRope(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
+// q4Matmul(ctx, x, ldx, rows, k, w, wBytes, n, y, ldy): y = x W^T over a tile32-compact Q4_0
+// tensor (qattn_q4_matmul).
+napi_value Q4Matmul(napi_env env, napi_callback_info info) {
+  napi_value argv[10];
+  if (!args_of(env, info, 10, argv)) return nullptr;
+  Ctx* c = live_ctx(env, argv[0]);
+  if (!c) return nullptr;
+  Buf* x = live_buf(env, argv[1]);
+  Buf* w = x ? live_buf(env, argv[5]) : nullptr;
+  Buf* y = w ? live_buf(env, argv[8]) : nullptr;
+  if (!y) return nullptr;
+  int64_t ldx, rows, k, wbytes, n, ldy;
+  if (!get_i64(env, argv[2], &ldx) || !get_i64(env, argv[3], &rows) || !get_i64(env, argv[4], &k) ||
+      !get_i64(env, argv[6], &wbytes) || !get_i64(env, argv[7], &n) || !get_i64(env, argv[9], &ldy) || rows < 0 ||
+      rows > INT32_MAX || k < 0 || k > INT32_MAX || n < 0 || n > INT32_MAX) {
+    napi_throw_type_error(env, nullptr, "expected (ctx, x, ldx, rows, k, w, wBytes, n, y, ldy)");
+    return nullptr;
+  }
+  if ((size_t)rows * (size_t)ldx * 2 > x->bytes || (size_t)rows * (size_t)ldy * 2 > y->bytes || (size_t)wbytes > w->bytes) {
+    napi_throw_range_error(env, nullptr, "rows exceed the buffers");
+    return nullptr;
+  }
+  int rc = qattn_q4_matmul(c->ctx, x->ptr, ldx, (int32_t)rows, (int32_t)k, w->ptr, wbytes, (int32_t)n, y->ptr, ldy,
+                           nullptr);
+  if (rc) return throw_qattn(env, rc, c->ctx);
+  return undefined(env);
+}
+
 // poolLastL2(ctx, x, rowStride, width, cuSeqlens, out): out (f32 rows of `width`) receives the
 // L2-normalised last row of each sequence of x (fp16 rows of rowStride elements).
 napi_value PoolLastL2(napi_env env, napi_callback_info info) {
@@ -664,7 +692,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"planDescribe", PlanDescribe}, {"planMask", PlanMask},
       {"debugMask", DebugMask},       {"genQkv", GenQkv},
       {"fillTokenRows", FillTokenRows}, {"qkNormRope", QkNormRope},
-      {"poolLastL2", PoolLastL2},
+      {"poolLastL2", PoolLastL2},     {"q4Matmul", Q4Matmul},
       {"synchronize", Synchronize},   {"synchronizeAsync", SynchronizeAsync},
   };
   for (const Fn& f : fns) {

@@ -1,15 +1,17 @@
 'use strict';
 // Node entry point of the MI355X attention path (the reference's src/webgpu engine surface).
 const { Qwen3EmbeddingEngine, packPadded, packVarlen, cuSeqlensOf } = require('./embedding-engine');
-const { DeviceContext, DeviceBuffer, CausalAttentionKernel, MASK } = require('./ops');
+const { DeviceContext, DeviceBuffer, CausalAttentionKernel, CompactQ4Matmul, MASK } = require('./ops');
 const { HipAttentionRuntime, HipAttentionPlan } = require('./runtime');
 const { loadAddon } = require('./addon');
+const prepacked = require('./prepacked');
 
 module.exports = {
   Qwen3EmbeddingEngine,
   HipAttentionRuntime,
   HipAttentionPlan,
   CausalAttentionKernel,
+  CompactQ4Matmul,
   DeviceContext,
   DeviceBuffer,
   MASK,
@@ -17,4 +19,5 @@ module.exports = {
   packVarlen,
   cuSeqlensOf,
   loadAddon,
+  prepacked,
 };

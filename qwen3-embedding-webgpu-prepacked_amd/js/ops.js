@@ -90,4 +90,31 @@ class CausalAttentionKernel {
   }
 }
 
-module.exports = { DeviceContext, DeviceBuffer, CausalAttentionKernel, MASK };
+// The projection over a `.wgpack` Q4_0 tensor (the reference's compact batch matmul,
+// src/webgpu/quant-matmul.ts:267-307, and its `matmul(input, name, rows, output)` helper):
+// upload(model, name) places a parsed file's q4_0-tile32-compact tensor [K, N] on the device as
+// it is stored; run(x, rows, y) computes y = x W^T for fp16 rows x [rows, K] into y [rows, N].
+class CompactQ4Matmul {
+  constructor(context) {
+    this.context = context;
+  }
+
+  upload(model, name) {
+    const t = model.tensors.get(name);
+    if (!t) throw new Error(`prepacked model has no tensor ${name}`);
+    if (t.storage !== 'q4_0-tile32-compact') throw new Error(`${name} is not a compact Q4_0 tensor`);
+    const [k, n] = t.dimensions;
+    const buffer = this.context.alloc(t.byteLength);
+    buffer.write(new Uint8Array(model.buffer, t.byteOffset, t.byteLength));
+    return { name, k, n, buffer };
+  }
+
+  run(x, rows, weight, y, options = {}) {
+    const ldx = options.inputStride === undefined ? weight.k : options.inputStride;
+    const ldy = options.outputStride === undefined ? weight.n : options.outputStride;
+    this.context.addon.q4Matmul(this.context.handle, x.handle, ldx, rows, weight.k, weight.buffer.handle,
+      weight.buffer.bytes, weight.n, y.handle, ldy);
+  }
+}
+
+module.exports = { DeviceContext, DeviceBuffer, CausalAttentionKernel, CompactQ4Matmul, MASK };

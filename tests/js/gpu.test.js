@@ -125,6 +125,47 @@ test('device pool (poolLastL2) equals the host L2 normalisation of the o_last ro
   runtime.plans = [];
 });
 
+test('.wgpack compact Q4_0 tensor -> device -> CompactQ4Matmul equals the host product exactly', () => {
+  const fmt = pkg.prepacked;
+  // K = 64, N = 40 (two tiles, the second partial), scale 2^-5, x in {-2..2}: every product and
+  // partial sum is a multiple of 2^-5 below 64, exact in fp32 and fp16, so the result is exact.
+  const k = 64, n = 40, rows = 9;
+  const raw = new Uint8Array(n * 2 * 18);
+  let seed = 12345;
+  const rnd = () => { seed = (seed * 1103515245 + 12345) & 0x7fffffff; return seed >> 8; };
+  for (let b = 0; b < n * 2; b += 1) {
+    raw[b * 18] = 0x00; raw[b * 18 + 1] = 0x28;  // f16 0x2800 = 2^-5
+    for (let j = 2; j < 18; j += 1) raw[b * 18 + j] = rnd() & 255;
+  }
+  const packed = fmt.packQ40Tile32('blk.0.attn_qkv.weight', [{ name: 'w', k, n, bytes: raw }]);
+  const file = fmt.buildPrepackedFile('0', 0, {}, [packed]);
+  const model = fmt.parsePrepackedModel(file.buffer);
+  const mm = new pkg.CompactQ4Matmul(ctx);
+  const weight = mm.upload(model, 'blk.0.attn_qkv.weight');
+  const xs = Array.from({ length: rows * k }, () => (rnd() % 5) - 2);
+  const halves = { '-2': 0xc000, '-1': 0xbc00, '0': 0x0000, '1': 0x3c00, '2': 0x4000 };
+  const x = ctx.alloc(rows * k * 2);
+  x.write(Uint16Array.from(xs, (v) => halves[String(v)]));
+  const ldy = 40;
+  const y = ctx.alloc(rows * ldy * 2);
+  mm.run(x, rows, weight, y);
+  ctx.synchronize();
+  const got = y.read(new Uint16Array(rows * ldy));
+  const f16 = (h) => { const e = (h >> 10) & 31, m = h & 1023, sgn = h & 0x8000 ? -1 : 1;
+    return e === 0 ? sgn * m * 2 ** -24 : sgn * (1 + m / 1024) * 2 ** (e - 15); };
+  for (let r = 0; r < rows; r += 1) for (let c = 0; c < n; c += 1) {
+    let want = 0;
+    for (let kk = 0; kk < k; kk += 1) {
+      const block = (c * 2 + (kk >> 5)) * 18, j = kk & 31;
+      const byte = raw[block + 2 + (j & 15)];
+      const q = j < 16 ? byte & 15 : byte >> 4;
+      want += xs[r * k + kk] * (q - 8) * 2 ** -5;
+    }
+    assert.strictEqual(f16(got[r * ldy + c]), want, `row ${r} col ${c}`);
+  }
+  for (const b of [x, y, weight.buffer]) b.destroy();
+});
+
 test('plan.run rejects malformed input before launching', async () => {
   const runtime = new HipAttentionRuntime({ context: ctx, layers: 1 });
   const plan = runtime.createPlan(2, 4);

@@ -21,3 +21,36 @@ def test_node_engine_and_boundary():
                        text=True, timeout=120, env=env)
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr
+
+
+@pytest.mark.skipif(shutil.which("node") is None, reason="node is not installed")
+def test_node_prepacked_format():
+    r = subprocess.run(["node", os.path.join(HERE, "js", "prepacked.test.js")], capture_output=True,
+                       text=True, timeout=120)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+
+
+@pytest.mark.skipif(shutil.which("node") is None, reason="node is not installed")
+def test_node_packer_equals_oracle_packer(oracle, tmp_path):
+    # Two parts (70 and 33 rows, K = 96) of seeded GGML Q4_0 bytes, packed by js/prepacked.js and by
+    # the oracle's restatement of format.ts:64-96: identical bytes.
+    import numpy as np
+    rng = np.random.default_rng(17)
+    k = 96
+    a = rng.integers(0, 256, size=70 * 3 * 18, dtype=np.uint8)
+    b = rng.integers(0, 256, size=33 * 3 * 18, dtype=np.uint8)
+    (tmp_path / "a.bin").write_bytes(a.tobytes())
+    (tmp_path / "b.bin").write_bytes(b.tobytes())
+    mod = os.path.join(HERE, "..", "qwen3-embedding-webgpu-prepacked_amd", "js", "prepacked.js")
+    script = (
+        f"const fmt = require({mod!r}); const fs = require('fs');"
+        f"const rd = (f) => new Uint8Array(fs.readFileSync(f));"
+        f"const p = fmt.packQ40Tile32('w', [{{name: 'a', k: {k}, n: 70, bytes: rd({str(tmp_path / 'a.bin')!r})}},"
+        f"  {{name: 'b', k: {k}, n: 33, bytes: rd({str(tmp_path / 'b.bin')!r})}}]);"
+        f"fs.writeFileSync({str(tmp_path / 'out.bin')!r}, Buffer.from(p.bytes));")
+    r = subprocess.run(["node", "-e", script], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr
+    got = np.frombuffer((tmp_path / "out.bin").read_bytes(), np.uint8)
+    want, _, n = oracle.pack_q40_tile32([(k, 70, a.tobytes()), (k, 33, b.tobytes())])
+    assert n == 103 and np.array_equal(got, want)
