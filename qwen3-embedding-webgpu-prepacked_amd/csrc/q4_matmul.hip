@@ -65,108 +65,154 @@ __device__ inline h8 dequant8(u2 q, h2 scale) {
   return h8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// LDS tiles: 128 rows x 32 columns of fp16 (64 B per row) for X (A) and for the dequantised
+// weights (B, row = output column n).  The four 16-byte chunks of row r sit at physical chunk
+// c ^ ((r >> 2) & 3): 16 consecutive rows reading one logical chunk then cover all 64 banks, so
+// the fragment reads (lanes 0-15 / 16-31 / ... take 16 consecutive rows) are conflict free.
+constexpr int kQ4TileBytes = kQ4Tile * 64;  // 8 KiB
+__device__ inline uint32_t q4_lds_off(int row, int chunk) { return row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4); }
+
 __global__ __launch_bounds__(256, 2) void q4_matmul_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, int K,
                                                            const uint8_t* __restrict__ w, uint32_t w_bytes, int N,
                                                            _Float16* __restrict__ y, int64_t ldy, int tiles_n,
                                                            int tiles_total, int per_xcd) {
+  // Double-buffered A and B tiles: four distinct objects, each buffer choice fixed at compile
+  // time, so the compiler sees that LDS-DMA writes in flight never alias the tile being read.
+  __shared__ __attribute__((aligned(1024))) char sA0[kQ4TileBytes];
+  __shared__ __attribute__((aligned(1024))) char sA1[kQ4TileBytes];
+  __shared__ __attribute__((aligned(1024))) char sB0[kQ4TileBytes];
+  __shared__ __attribute__((aligned(1024))) char sB1[kQ4TileBytes];
+
   // Tile of this workgroup: XCD b % 8 owns tiles [xcd * per_xcd, (xcd + 1) * per_xcd).
   const int b = blockIdx.x;
   const int t = (b & 7) * per_xcd + (b >> 3);
-  if (b >> 3 >= per_xcd || t >= tiles_total) return;
+  if (t >= tiles_total) return;
   const int m0 = (t / tiles_n) * kQ4Tile, n0 = (t % tiles_n) * kQ4Tile;
 
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hl = lane >> 5;
-  const int wm = m0 + 64 * (wave & 1), wn = n0 + 64 * (wave >> 1);
+  const int wr = 64 * (wave & 1), wc = 64 * (wave >> 1);  // this wave's 64 x 64 inside the tile
   const int kblocks = K >> 5;
 
-  // X rows of the run (rows >= M read as zeros), the weight tensor, Y rows.
-  const auto xrs = q4_rsrc(x, (uint32_t)M * (uint32_t)ldx * 2u);
+  const auto xrs = q4_rsrc(x, (uint32_t)M * (uint32_t)ldx * 2u);  // rows >= M read as zeros
   const auto wrs = q4_rsrc(w, w_bytes);
   const auto yrs = q4_rsrc(y, (uint32_t)M * (uint32_t)ldy * 2u);
 
-  // A fragment (mb, s): row wm + 32 mb + l32, columns 32 kb + 16 s + 8 hl .. +7.
-  uint32_t a_off[2];
+  // ---- A: LDS-DMA, 16 B per lane per instruction, 1 KiB (16 rows) per wave instruction.
+  // Instruction j of wave `wave` fills rows 16 (2 wave + j) .. +15; lane's LDS slot p = lane * 16
+  // within that KiB is row 16 (2 wave + j) + lane / 4, physical chunk lane & 3, which holds
+  // logical chunk (lane & 3) ^ ((row >> 2) & 3): columns 8 * that .. +7 of the K block.
+  uint32_t a_src[2];
 #pragma unroll
-  for (int mb = 0; mb < 2; ++mb) a_off[mb] = (uint32_t)(wm + 32 * mb + l32) * (uint32_t)ldx * 2u + 16u * hl;
-  // Weight record of (row n = wn + 32 nb + l32, block kb): (((n / 32) * kblocks + kb) * 32 + l32) * 20.
-  uint32_t w_off[2];
+  for (int j = 0; j < 2; ++j) {
+    const int row = 16 * (2 * wave + j) + (lane >> 2);
+    const int chunk = (lane & 3) ^ ((row >> 2) & 3);
+    a_src[j] = (uint32_t)(m0 + row) * (uint32_t)ldx * 2u + 16u * chunk;
+  }
+  auto load_a = [&](char* dst, int kb) {
+    kb = kb < kblocks ? kb : kblocks - 1;  // past the end: re-read the last block (never used)
 #pragma unroll
-  for (int nb = 0; nb < 2; ++nb)
-    w_off[nb] = ((uint32_t)((wn >> 5) + nb) * (uint32_t)kblocks * 32u + (uint32_t)l32) * kQ4Record;
-  const uint32_t w_step = 32u * kQ4Record;  // next K block of the same row
-
-  auto load = [&](int kb, h8 (&a)[2][2], uint32_t (&sc)[2], u2 (&q)[2]) {
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-        a[mb][s] = __builtin_bit_cast(
-            h8, __builtin_amdgcn_raw_buffer_load_b128(xrs, a_off[mb] + (uint32_t)kb * 64u + 32u * s, 0, 0));
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const uint32_t r = w_off[nb] + (uint32_t)kb * w_step;
-      sc[nb] = __builtin_amdgcn_raw_buffer_load_b32(wrs, r, 0, 0);
-      q[nb] = __builtin_amdgcn_raw_buffer_load_b64(wrs, r + 4u + 8u * hl, 0, 0);
-    }
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_void_t*)(dst + 1024 * (2 * wave + j)), 16,
+                                               a_src[j] + (uint32_t)kb * 64u, 0, 0, 0);
   };
 
+  // ---- B: thread (row n = tid / 2, half h = tid & 1) owns quant bytes 8h .. 8h+7 of the record
+  // of (n0 + n, kb): their low nibbles are columns 8h .. +7 (chunk h), their high nibbles columns
+  // 16 + 8h .. +7 (chunk 2 + h).  Records of rows past the tensor read as zeros.
+  const int brow = tid >> 1, bhalf = tid & 1;
+  const uint32_t w_rec = ((uint32_t)((n0 + brow) >> 5) * (uint32_t)kblocks * 32u + (uint32_t)((n0 + brow) & 31)) *
+                         kQ4Record;
+  const uint32_t w_step = 32u * kQ4Record;
+  const uint32_t b_lo = q4_lds_off(brow, bhalf), b_hi = q4_lds_off(brow, 2 + bhalf);
+  struct WRegs {
+    uint32_t scale;
+    u2 q;
+  };
+  auto load_w = [&](WRegs& r, int kb) {
+    kb = kb < kblocks ? kb : kblocks - 1;
+    const uint32_t off = w_rec + (uint32_t)kb * w_step;
+    r.scale = __builtin_amdgcn_raw_buffer_load_b32(wrs, off, 0, 0);
+    r.q = __builtin_amdgcn_raw_buffer_load_b64(wrs, off + 4u + 8u * bhalf, 0, 0);
+  };
+  auto store_b = [&](char* dst, const WRegs& r) {
+    const _Float16 s = __builtin_bit_cast(h2, r.scale)[0];
+    const h2 scale = {s, s};
+    *reinterpret_cast<h8*>(dst + b_lo) = dequant8<false>(r.q, scale);
+    *reinterpret_cast<h8*>(dst + b_hi) = dequant8<true>(r.q, scale);
+  };
+
+  // ---- fragments: lane reads row (wr or wc) + 32 blk + l32, logical chunk 2 s + hl.
   f16x acc[2][2];
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = f16x{};
-
-  constexpr int kStages = 4;
-  h8 a[kStages][2][2];
-  uint32_t sc[kStages][2];
-  u2 q[kStages][2];
-  auto load_stage = [&](auto sconst, int kb) {
-    constexpr int S = decltype(sconst)::value;
-    load(kb < kblocks ? kb : kblocks - 1, a[S], sc[S], q[S]);
-  };
-  auto compute_stage = [&](auto sconst) {
-    constexpr int S = decltype(sconst)::value;
+  auto compute = [&](const char* a_t, const char* b_t) {
+    h8 af[2][2], bf[2][2];
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const _Float16 s = __builtin_bit_cast(h2, sc[S][nb])[0];
-      const h2 scale = {s, s};
-      const h8 b_lo = dequant8<false>(q[S][nb], scale);  // columns 8 hl .. +7 of the block
-      const h8 b_hi = dequant8<true>(q[S][nb], scale);   // columns 16 + 8 hl .. +7
+    for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
-        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[S][mb][0], b_lo, acc[mb][nb], 0, 0, 0);
-        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[S][mb][1], b_hi, acc[mb][nb], 0, 0, 0);
+      for (int s = 0; s < 2; ++s) {
+        af[blk][s] = *reinterpret_cast<const h8*>(a_t + q4_lds_off(wr + 32 * blk + l32, 2 * s + hl));
+        bf[blk][s] = *reinterpret_cast<const h8*>(b_t + q4_lds_off(wc + 32 * blk + l32, 2 * s + hl));
       }
-    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+          acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[mb][s], bf[nb][s], acc[mb][nb], 0, 0, 0);
   };
-  using S0 = std::integral_constant<int, 0>;
-  using S1 = std::integral_constant<int, 1>;
-  using S2 = std::integral_constant<int, 2>;
-  using S3 = std::integral_constant<int, 3>;
-  // Step kb: issue block kb + 3 into stage (kb + 3) % 4, then compute block kb from stage kb % 4.
-  auto step = [&](auto cur, auto ahead, int kb) {
-    load_stage(ahead, kb + 3);
-    if (kb < kblocks) compute_stage(cur);
+
+  // ---- pipeline.  Step kb (P = kb & 1, compile time): issue A(kb+1) into sA<1-P> and W(kb+3)
+  // into register stage (kb+3) % 4; compute block kb from sA<P>, sB<P>; dequantise W(kb+1)
+  // (loaded two steps ago) into sB<1-P>; wait for A(kb+1) (only W(kb+3), issued after it, may
+  // still be in flight: vmcnt(2)); barrier.  Every load is issued (clamped past the end), so the
+  // counts are the same on every path.
+  WRegs wreg[4];
+  load_a(sA0, 0);
+  load_w(wreg[0], 0);
+  load_w(wreg[1], 1);
+  load_w(wreg[2], 2);
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8) | 4);  // vmcnt(4): A(0), W(0) landed
+  store_b(sB0, wreg[0]);
+  __syncthreads();
+  auto step = [&](auto pconst, auto wcur, auto wnext, int kb) {
+    constexpr int P = decltype(pconst)::value;
+    constexpr int WN = decltype(wnext)::value;   // stage of W(kb+1)
+    constexpr int WA = decltype(wcur)::value;    // stage receiving W(kb+3)
+    char* const a_cur = P == 0 ? sA0 : sA1;
+    char* const a_nxt = P == 0 ? sA1 : sA0;
+    char* const b_cur = P == 0 ? sB0 : sB1;
+    char* const b_nxt = P == 0 ? sB1 : sB0;
+    load_a(a_nxt, kb + 1);
+    load_w(wreg[WA], kb + 3);
+    if (kb < kblocks) compute(a_cur, b_cur);
+    store_b(b_nxt, wreg[WN]);
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8) | 2);  // vmcnt(2)
+    __syncthreads();
   };
-  // Prologue in stage order (the scheduler may not interleave the stages: the loop's waits count
-  // on stage 0 being the oldest in flight on entry, as it is on every back edge).
-  load_stage(S0{}, 0);
-  __builtin_amdgcn_sched_barrier(0);
-  load_stage(S1{}, 1);
-  __builtin_amdgcn_sched_barrier(0);
-  load_stage(S2{}, 2);
-  __builtin_amdgcn_sched_barrier(0);
-  for (int kb = 0; kb < kblocks; kb += kStages) {
-    step(S0{}, S3{}, kb);
-    step(S1{}, S0{}, kb + 1);
-    step(S2{}, S1{}, kb + 2);
-    step(S3{}, S2{}, kb + 3);
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  for (int kb = 0; kb < kblocks; kb += 4) {
+    step(I0{}, I3{}, I1{}, kb);
+    step(I1{}, I0{}, I2{}, kb + 1);
+    step(I0{}, I1{}, I3{}, kb + 2);
+    step(I1{}, I2{}, I0{}, kb + 3);
   }
+  __builtin_amdgcn_s_waitcnt(0);  // the clamped loads past the end land before the LDS is released
 
   // D (32 x 32 per block): lane holds column l32 and rows 8 (r / 4) + 4 hl + r % 4, r = 0..15.
   // Columns >= N are skipped here; rows >= M fall outside the Y resource and are dropped.
+  const int wm = m0 + wr, wn = n0 + wc;
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
     const int n = wn + 32 * nb + l32;
