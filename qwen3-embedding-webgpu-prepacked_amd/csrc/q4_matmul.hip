@@ -152,29 +152,38 @@ __global__ __launch_bounds__(256, 2) void q4_matmul_kernel(const _Float16* __res
   for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = f16x{};
-  auto compute = [&](const char* a_t, const char* b_t) {
-    h8 af[2][2], bf[2][2];
+  // Fragments of one K block: two sets, alternating by block parity, so the next block's reads
+  // are in flight while this block's MFMAs run.
+  struct Frags {
+    h8 a[2][2], b[2][2];
+  };
+  Frags frag[2];
+  auto read_frags = [&](const char* a_t, const char* b_t, Frags& f) {
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        af[blk][s] = *reinterpret_cast<const h8*>(a_t + q4_lds_off(wr + 32 * blk + l32, 2 * s + hl));
-        bf[blk][s] = *reinterpret_cast<const h8*>(b_t + q4_lds_off(wc + 32 * blk + l32, 2 * s + hl));
+        f.a[blk][s] = *reinterpret_cast<const h8*>(a_t + q4_lds_off(wr + 32 * blk + l32, 2 * s + hl));
+        f.b[blk][s] = *reinterpret_cast<const h8*>(b_t + q4_lds_off(wc + 32 * blk + l32, 2 * s + hl));
       }
+  };
+  auto mma = [&](const Frags& f) {
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb)
-          acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[mb][s], bf[nb][s], acc[mb][nb], 0, 0, 0);
+          acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[mb][s], f.b[nb][s], acc[mb][nb], 0, 0, 0);
   };
 
   // ---- pipeline.  Step kb (P = kb & 1, compile time): issue A(kb+1) into sA<1-P> and W(kb+3)
-  // into register stage (kb+3) % 4; compute block kb from sA<P>, sB<P>; dequantise W(kb+1)
-  // (loaded two steps ago) into sB<1-P>; wait for A(kb+1) (only W(kb+3), issued after it, may
-  // still be in flight: vmcnt(2)); barrier.  Every load is issued (clamped past the end), so the
-  // counts are the same on every path.
+  // into register stage (kb+3) % 4; dequantise W(kb+1) (loaded two steps ago) into sB<1-P>; run
+  // block kb's MFMAs on the fragments read at the end of the previous step; wait for A(kb+1)
+  // (only W(kb+3), issued after it, may still be in flight: vmcnt(2)); barrier; read block
+  // kb+1's fragments.  sB<1-P> is free at its write: its last reads (block kb-1's fragments)
+  // were consumed by MFMAs before the previous barrier.  Every load is issued (clamped past the
+  // end), so the counts are the same on every path.
   WRegs wreg[4];
   load_a(sA0, 0);
   load_w(wreg[0], 0);
@@ -183,20 +192,20 @@ __global__ __launch_bounds__(256, 2) void q4_matmul_kernel(const _Float16* __res
   __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8) | 4);  // vmcnt(4): A(0), W(0) landed
   store_b(sB0, wreg[0]);
   __syncthreads();
+  read_frags(sA0, sB0, frag[0]);
   auto step = [&](auto pconst, auto wcur, auto wnext, int kb) {
     constexpr int P = decltype(pconst)::value;
     constexpr int WN = decltype(wnext)::value;   // stage of W(kb+1)
     constexpr int WA = decltype(wcur)::value;    // stage receiving W(kb+3)
-    char* const a_cur = P == 0 ? sA0 : sA1;
     char* const a_nxt = P == 0 ? sA1 : sA0;
-    char* const b_cur = P == 0 ? sB0 : sB1;
     char* const b_nxt = P == 0 ? sB1 : sB0;
     load_a(a_nxt, kb + 1);
     load_w(wreg[WA], kb + 3);
-    if (kb < kblocks) compute(a_cur, b_cur);
     store_b(b_nxt, wreg[WN]);
+    if (kb < kblocks) mma(frag[P]);
     __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8) | 2);  // vmcnt(2)
     __syncthreads();
+    read_frags(a_nxt, b_nxt, frag[1 - P]);
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
