@@ -81,3 +81,43 @@ export class HipAttentionRuntime implements EmbeddingRuntime {
   createPlan(batch: number, sequence: number): EmbeddingPlan;
   destroy(): void;
 }
+
+// ---- the `.wgpack` container (the reference's src/prepacked/format.ts) and the Q4_0 projection.
+export interface PackedTensorBytes {
+  name: string; dimensions: number[]; type: number;
+  storage: 'q4_0-tile32-compact' | 'raw'; bytes: Uint8Array;
+}
+export interface PrepackedTensorHeader {
+  name: string; dimensions: number[]; type: number; storage: 'q4_0-tile32-compact' | 'raw';
+  offset: number; byteLength: number;
+}
+export interface PrepackedModel {
+  header: {
+    version: 2; sourceSha256: string; sourceBytes: number; layout: 'q4_0-tile32-compact-v2';
+    tileRows: 32; blockValues: 32; blockBytes: 20;
+    metadata: Record<string, string | number | boolean | Array<string | number | boolean>>;
+    tensors: PrepackedTensorHeader[];
+  };
+  tensors: Map<string, PrepackedTensorHeader & { byteOffset: number }>;
+  buffer: ArrayBuffer;
+  dataOffset: number;
+}
+export const prepacked: {
+  MAGIC: 'WGPACK02'; LAYOUT: 'q4_0-tile32-compact-v2'; TILE_ROWS: 32; BLOCK_VALUES: 32; BLOCK_BYTES: 20;
+  STORAGE_COMPACT: 'q4_0-tile32-compact'; STORAGE_RAW: 'raw'; GGML_TYPE: { F32: 0; F16: 1; Q4_0: 2 };
+  packQ40Tile32(name: string, parts: ReadonlyArray<{ name: string; k: number; n: number; bytes: Uint8Array }>): PackedTensorBytes;
+  rawTensor(name: string, dimensions: number[], type: number, bytes: Uint8Array): PackedTensorBytes;
+  buildPrepackedFile(sourceSha256: string, sourceBytes: number,
+                     metadata: PrepackedModel['header']['metadata'], tensors: ReadonlyArray<PackedTensorBytes>): Uint8Array;
+  parsePrepackedModel(buffer: ArrayBuffer): PrepackedModel;
+  tensorBytes(model: PrepackedModel, name: string): Uint8Array;
+};
+
+export interface CompactQ4Weight { name: string; k: number; n: number; buffer: DeviceBuffer }
+/** y = x W^T over a compact Q4_0 tensor (the reference's compact batch matmul). */
+export class CompactQ4Matmul {
+  constructor(context: DeviceContext);
+  upload(model: PrepackedModel, name: string): CompactQ4Weight;
+  run(x: DeviceBuffer, rows: number, weight: CompactQ4Weight, y: DeviceBuffer,
+      options?: { inputStride?: number; outputStride?: number }): void;
+}
