@@ -249,3 +249,14 @@ def test_q4_compact_bytes(qattn, oracle):
     # the oracle's packer writes exactly that many bytes
     packed, k, n = oracle.pack_q40_tile32([(96, 70, bytes(70 * 3 * 18))])
     assert packed.size == f(96, 70)
+
+
+def test_consumer_and_projection_entry_points_reject_null_before_any_device_use(qattn):
+    # No context, no device: both entry points validate on the host and return EINVAL.
+    import numpy as np
+    lib = qattn.lib()
+    cu = np.array([0, 3], np.int32)
+    assert lib.qattn_pool_last_l2(None, FAKE, 1024, 1024, cu.ctypes.data, 1, FAKE, 1024, None) == qattn.EINVAL
+    assert b"NULL" in lib.qattn_last_error(None)
+    assert lib.qattn_q4_matmul(None, FAKE, 64, 4, 64, FAKE, 2560, 8, FAKE, 8, None) == qattn.EINVAL
+    assert b"NULL" in lib.qattn_last_error(None)
