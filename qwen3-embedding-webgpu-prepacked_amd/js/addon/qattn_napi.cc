@@ -11,6 +11,7 @@
 
 #include <cstdint>
 #include <cstring>
+#include <set>
 #include <string>
 #include <vector>
 
@@ -30,8 +31,19 @@ namespace {
     }                                                                            \
   } while (0)
 
+// Lifetime.  A context's JS handle, and every buffer and run made from it, each hold one
+// reference on its Ctx; the Ctx is deleted when the last of them is finalized, whatever order the
+// garbage collector (or environment teardown) finalizes them in.  The device context itself
+// (qattn_ctx) lives until destroyContext() or the last reference: destroyContext() first releases
+// every run and buffer still alive on it (runs synchronize on the context stream, so they go
+// before the context), and their handles then report "destroyed" instead of touching freed memory.
+struct Buf;
+struct Run;
 struct Ctx {
   qattn_ctx* ctx = nullptr;
+  int refs = 1;  // the context handle's own reference
+  std::set<Buf*> bufs;
+  std::set<Run*> runs;
 };
 struct Buf {
   Ctx* owner = nullptr;
@@ -39,8 +51,17 @@ struct Buf {
   size_t bytes = 0;
 };
 struct Run {
+  Ctx* owner = nullptr;
   qattn_run* run = nullptr;
 };
+
+void release_device(Ctx* c);
+void unref(Ctx* c) {
+  if (--c->refs == 0) {
+    release_device(c);
+    delete c;
+  }
+}
 
 napi_value throw_qattn(napi_env env, int rc, const qattn_ctx* ctx) {
   std::string msg = "qattn error " + std::to_string(rc) + ": " + qattn_last_error(ctx);
@@ -104,22 +125,41 @@ bool typed_bytes(napi_env env, napi_value v, void** data, size_t* bytes) {
   return false;
 }
 
-void finalize_ctx(napi_env, void* data, void*) {
-  auto* c = static_cast<Ctx*>(data);
-  if (c->ctx) qattn_destroy(c->ctx);
-  delete c;
+// Runs, then buffers, then the device context: everything still alive on `c`.
+void release_device(Ctx* c) {
+  if (!c->ctx) return;
+  for (Run* r : c->runs)
+    if (r->run) {
+      qattn_run_destroy(r->run);
+      r->run = nullptr;
+    }
+  for (Buf* b : c->bufs)
+    if (b->ptr) {
+      qattn_buffer_free(c->ctx, b->ptr);
+      b->ptr = nullptr;
+    }
+  qattn_destroy(c->ctx);
+  c->ctx = nullptr;
 }
+
+void finalize_ctx(napi_env, void* data, void*) { unref(static_cast<Ctx*>(data)); }
 void finalize_buf(napi_env, void* data, void*) {
   // Device memory is released by free(); a collected handle that was never freed is released
-  // here if its context still exists.
+  // here while its context is still alive.
   auto* b = static_cast<Buf*>(data);
-  if (b->ptr && b->owner && b->owner->ctx) qattn_buffer_free(b->owner->ctx, b->ptr);
+  Ctx* c = b->owner;
+  if (b->ptr && c->ctx) qattn_buffer_free(c->ctx, b->ptr);
+  c->bufs.erase(b);
   delete b;
+  unref(c);
 }
 void finalize_run(napi_env, void* data, void*) {
   auto* r = static_cast<Run*>(data);
-  if (r->run) qattn_run_destroy(r->run);
+  Ctx* c = r->owner;
+  if (r->run && c->ctx) qattn_run_destroy(r->run);
+  c->runs.erase(r);
   delete r;
+  unref(c);
 }
 
 napi_value args_of(napi_env env, napi_callback_info info, size_t want, napi_value* argv) {
@@ -155,8 +195,7 @@ napi_value DestroyContext(napi_env env, napi_callback_info info) {
   if (!args_of(env, info, 1, argv)) return nullptr;
   Ctx* c = get_external<Ctx>(env, argv[0], "context");
   if (!c) return nullptr;
-  if (c->ctx) qattn_destroy(c->ctx);
-  c->ctx = nullptr;
+  release_device(c);
   return undefined(env);
 }
 
@@ -203,6 +242,8 @@ napi_value Alloc(napi_env env, napi_callback_info info) {
   int rc = qattn_buffer_alloc(c->ctx, (size_t)bytes, &ptr);
   if (rc) return throw_qattn(env, rc, c->ctx);
   auto* b = new Buf{c, ptr, (size_t)bytes};
+  c->bufs.insert(b);
+  ++c->refs;
   napi_value out;
   NAPI_OK(env, napi_create_external(env, b, finalize_buf, nullptr, &out));
   return out;
@@ -294,13 +335,21 @@ bool get_i32_array(napi_env env, napi_value v, std::vector<int32_t>* out) {
   return true;
 }
 
-// Fills a qattn_run_desc from a JS descriptor object.  Device tensors are buffer externals with
-// optional byte offsets (qOffsetBytes, ...), strides in elements.
+// Fills a qattn_run_desc from a JS descriptor object.  Device tensors are buffer externals of
+// context `owner` with optional byte offsets (qOffsetBytes, ...), strides in elements.  With a
+// device, every tensor's extent -- the bytes the kernels can touch, from its offset, strides and
+// the token count -- is checked against its buffer (RangeError), as WebGPU validates bindings.
 bool read_desc(napi_env env, napi_value d, qattn_run_desc* desc, std::vector<int32_t>* cu,
-               bool need_device) {
+               const Ctx* owner) {
+  const bool need_device = owner != nullptr;
   std::memset(desc, 0, sizeof(*desc));
   napi_value v;
-  auto ptr_of = [&](const char* name, const char* off_name, const void** out, bool required) {
+  struct Binding {
+    const Buf* buf = nullptr;
+    int64_t off = 0;
+  };
+  auto ptr_of = [&](const char* name, const char* off_name, const void** out, bool required,
+                    Binding* bind) {
     if (!prop(env, d, name, &v)) {
       if (required) napi_throw_type_error(env, nullptr, (std::string("missing ") + name).c_str());
       return !required;
@@ -312,16 +361,28 @@ bool read_desc(napi_env env, napi_value d, qattn_run_desc* desc, std::vector<int
     }
     Buf* b = live_buf(env, v);
     if (!b) return false;
+    if (b->owner != owner) {
+      napi_throw_error(env, nullptr, (std::string(name) + " belongs to another context").c_str());
+      return false;
+    }
     int64_t off = 0;
     napi_value ov;
-    if (prop(env, d, off_name, &ov)) get_i64(env, ov, &off);
+    if (prop(env, d, off_name, &ov) && !get_i64(env, ov, &off)) off = -1;
+    if (off < 0 || (uint64_t)off >= b->bytes || off % 16 != 0) {
+      napi_throw_range_error(env, nullptr,
+                             (std::string(off_name) + " must be a multiple of 16 inside the buffer").c_str());
+      return false;
+    }
     *out = static_cast<const char*>(b->ptr) + off;
+    bind->buf = b;
+    bind->off = off;
     return true;
   };
   const void *q, *k, *vv, *o, *ol = nullptr;
-  if (!ptr_of("q", "qOffsetBytes", &q, true) || !ptr_of("k", "kOffsetBytes", &k, true) ||
-      !ptr_of("v", "vOffsetBytes", &vv, true) || !ptr_of("o", "oOffsetBytes", &o, true) ||
-      !ptr_of("oLast", "oLastOffsetBytes", &ol, false))
+  Binding bq, bk, bv, bo, bl;
+  if (!ptr_of("q", "qOffsetBytes", &q, true, &bq) || !ptr_of("k", "kOffsetBytes", &k, true, &bk) ||
+      !ptr_of("v", "vOffsetBytes", &vv, true, &bv) || !ptr_of("o", "oOffsetBytes", &o, true, &bo) ||
+      !ptr_of("oLast", "oLastOffsetBytes", &ol, false, &bl))
     return false;
   desc->q = q;
   desc->k = k;
@@ -348,6 +409,30 @@ bool read_desc(napi_env env, napi_value d, qattn_run_desc* desc, std::vector<int
   }
   desc->cu_seqlens = cu->data();
   desc->nseq = (int32_t)cu->size() - 1;
+  if (!need_device) return true;
+  // Extents.  Strides below the head widths, bad cu_seqlens etc. are the C ABI's to reject (with
+  // its message); here only what would let a valid-looking descriptor reach past a buffer.
+  const int64_t T = cu->back();
+  for (int32_t i = 0; i < desc->nseq; ++i)
+    if ((*cu)[i + 1] < (*cu)[i] || (*cu)[i] < 0) return true;  // the C ABI rejects it
+  if (T <= 0) return true;
+  if (desc->q_row_stride < 0 || desc->k_row_stride < 0 || desc->v_row_stride < 0 ||
+      desc->o_row_stride < 0 || desc->v_offset < 0 || T > ((int64_t)1 << 31))
+    return true;  // rejected by the C ABI
+  auto fits = [&](const Binding& b, int64_t elems, const char* name) {
+    if ((uint64_t)b.off + 2 * (uint64_t)elems > b.buf->bytes) {
+      napi_throw_range_error(env, nullptr,
+                             (std::string(name) + ": rows x stride exceed the device buffer").c_str());
+      return false;
+    }
+    return true;
+  };
+  if (!fits(bq, (T - 1) * desc->q_row_stride + 2048, "q") ||
+      !fits(bk, (T - 1) * desc->k_row_stride + 1024, "k") ||
+      !fits(bv, desc->v_offset + (T - 1) * desc->v_row_stride + 1024, "v") ||
+      !fits(bo, (T - 1) * desc->o_row_stride + 2048, "o"))
+    return false;
+  if (ol && !fits(bl, (int64_t)desc->nseq * 2048, "oLast")) return false;
   return true;
 }
 
@@ -378,11 +463,13 @@ napi_value CreateRun(napi_env env, napi_callback_info info) {
   if (!c) return nullptr;
   qattn_run_desc desc;
   std::vector<int32_t> cu;
-  if (!read_desc(env, argv[1], &desc, &cu, true)) return nullptr;
+  if (!read_desc(env, argv[1], &desc, &cu, c)) return nullptr;
   qattn_run* run = nullptr;
   int rc = qattn_run_create(c->ctx, &desc, &run);
   if (rc) return throw_qattn(env, rc, c->ctx);
-  auto* r = new Run{run};
+  auto* r = new Run{c, run};
+  c->runs.insert(r);
+  ++c->refs;
   napi_value out;
   NAPI_OK(env, napi_create_external(env, r, finalize_run, nullptr, &out));
   return out;
@@ -390,8 +477,8 @@ napi_value CreateRun(napi_env env, napi_callback_info info) {
 
 Run* live_run(napi_env env, napi_value v) {
   Run* r = get_external<Run>(env, v, "attention run");
-  if (r && !r->run) {
-    napi_throw_error(env, nullptr, "attention run was destroyed");
+  if (r && (!r->run || !r->owner->ctx)) {
+    napi_throw_error(env, nullptr, r->run ? "context was destroyed" : "attention run was destroyed");
     return nullptr;
   }
   return r;
@@ -413,7 +500,7 @@ napi_value DestroyRun(napi_env env, napi_callback_info info) {
   if (!args_of(env, info, 1, argv)) return nullptr;
   Run* r = get_external<Run>(env, argv[0], "attention run");
   if (!r) return nullptr;
-  if (r->run) qattn_run_destroy(r->run);
+  if (r->run && r->owner->ctx) qattn_run_destroy(r->run);
   r->run = nullptr;
   return undefined(env);
 }
@@ -435,7 +522,7 @@ napi_value PlanDescribe(napi_env env, napi_callback_info info) {
   if (!args_of(env, info, 1, argv)) return nullptr;
   qattn_run_desc desc;
   std::vector<int32_t> cu;
-  if (!read_desc(env, argv[0], &desc, &cu, false)) return nullptr;
+  if (!read_desc(env, argv[0], &desc, &cu, nullptr)) return nullptr;
   int32_t n = 0;
   qattn_run_info i{};
   int rc = qattn_plan_describe(&desc, nullptr, 0, &n, &i);
@@ -505,6 +592,11 @@ napi_value GenQkv(napi_env env, napi_callback_info info) {
   Buf *q = live_buf(env, argv[4]), *k = q ? live_buf(env, argv[5]) : nullptr,
       *v = k ? live_buf(env, argv[6]) : nullptr;
   if (!v) return nullptr;
+  const int64_t T = cu.back();
+  if (T < 0 || (uint64_t)T * 4096 > q->bytes || (uint64_t)T * 2048 > k->bytes || (uint64_t)T * 2048 > v->bytes) {
+    napi_throw_range_error(env, nullptr, "tokens x head widths exceed the q/k/v buffers");
+    return nullptr;
+  }
   int rc = qattn_gen_qkv(c->ctx, (uint32_t)config, (uint32_t)layer, cu.data(), (int32_t)cu.size() - 1,
                          q->ptr, 2048, k->ptr, 1024, v->ptr, 1024, nullptr);
   if (rc) return throw_qattn(env, rc, c->ctx);

@@ -174,6 +174,69 @@ test('plan.run rejects malformed input before launching', async () => {
   plan.destroy();
 });
 
+test('createRun / genQkv reject descriptors that reach past their buffers (RangeError) before any launch', () => {
+  const addon = ctx.addon;
+  const T = 100;
+  const bq = ctx.alloc(T * 4096), bk = ctx.alloc(T * 2048), bv = ctx.alloc(T * 2048), bo = ctx.alloc(T * 4096);
+  const qkv = ctx.alloc(T * 8192), qkvShort = ctx.alloc(T * 8192 - 16), short4 = ctx.alloc(T * 4096 - 16), short2 = ctx.alloc(T * 2048 - 16);
+  const cuSeqlens = new Int32Array([0, 40, T]);
+  const base = { q: bq.handle, k: bk.handle, v: bv.handle, o: bo.handle, cuSeqlens, mask: 0 };
+  const run = addon.createRun(ctx.handle, base);  // exact sizes are accepted
+  addon.destroyRun(run);
+  const bad = [
+    Object.assign({}, base, { q: short4.handle }),
+    Object.assign({}, base, { k: short2.handle }),
+    Object.assign({}, base, { v: short2.handle }),
+    Object.assign({}, base, { o: short4.handle }),
+    Object.assign({}, base, { qOffsetBytes: 16 }),
+    Object.assign({}, base, { qOffsetBytes: T * 4096 }),
+    Object.assign({}, base, { kOffsetBytes: 8 }),
+    Object.assign({}, base, { oLast: short2.handle, oLastOffsetBytes: T * 2048 - 32 }),
+    // the reference's qkvRaw layout (V in place: stride 4096, offset 3072) one row short
+    Object.assign({}, base, { v: qkvShort.handle, vRowStride: 4096, vOffset: 3072 }),
+    Object.assign({}, base, { q: qkvShort.handle, qRowStride: 4096, k: qkvShort.handle, kRowStride: 4096, kOffsetBytes: 4096, v: qkvShort.handle, vRowStride: 4096, vOffset: 3072 }),
+  ];
+  for (const d of bad) assert.throws(() => addon.createRun(ctx.handle, d), RangeError);
+  const inPlace = addon.createRun(ctx.handle, Object.assign({}, base, {
+    q: qkv.handle, qRowStride: 4096, k: qkv.handle, kRowStride: 4096, kOffsetBytes: 4096, v: qkv.handle, vRowStride: 4096, vOffset: 3072 }));
+  addon.destroyRun(inPlace);
+  assert.throws(() => addon.genQkv(ctx.handle, 1, 0, cuSeqlens, short4.handle, bk.handle, bv.handle), RangeError);
+  assert.throws(() => addon.genQkv(ctx.handle, 1, 0, cuSeqlens, bq.handle, bk.handle, short2.handle), RangeError);
+  const other = new DeviceContext(0);
+  const foreign = other.alloc(T * 4096);
+  assert.throws(() => addon.createRun(ctx.handle, Object.assign({}, base, { q: foreign.handle })), /another context/);
+  other.destroy();
+  for (const b of [bq, bk, bv, bo, qkv, qkvShort, short4, short2]) b.destroy();
+});
+
+test('destroying a context before its buffers and runs: they throw afterwards, nothing is used after free', () => {
+  const c2 = new DeviceContext(0);
+  const attention = new CausalAttentionKernel(c2);
+  const T = 70;
+  const bufs = [c2.alloc(T * 4096), c2.alloc(T * 2048), c2.alloc(T * 2048), c2.alloc(T * 4096)];
+  const run = attention.createVarlenRun(bufs[0], bufs[1], bufs[2], bufs[3], [0, T], { mask: 'causal' });
+  c2.destroy();
+  assert.throws(() => attention.encode(run), /destroyed/);
+  assert.throws(() => c2.addon.runInfo(run.handle), /destroyed/);
+  assert.throws(() => bufs[0].read(new Uint16Array(8)), /freed/);
+  attention.destroyRun(run);  // no-ops once the context is gone
+  for (const b of bufs) b.destroy();
+});
+
+test('handles dropped without destroy() are finalized in any order without faults', async () => {
+  for (let round = 0; round < 3; round += 1) {
+    (() => {
+      const c2 = new DeviceContext(0);
+      const attention = new CausalAttentionKernel(c2);
+      const bufs = [c2.alloc(64 * 4096), c2.alloc(64 * 2048), c2.alloc(64 * 2048), c2.alloc(64 * 4096)];
+      attention.createVarlenRun(bufs[0], bufs[1], bufs[2], bufs[3], [0, 64], { mask: 'causal' });
+    })();
+    if (global.gc) global.gc();
+    await new Promise((r) => setImmediate(r));
+  }
+  ctx.synchronize();
+});
+
 (async () => {
   let failed = 0;
   for (const c of cases) {

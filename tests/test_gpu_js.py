@@ -21,7 +21,7 @@ def test_node_gpu_path(oracle, tmp_path):
     q, k, v = oracle.gen_qkv(1, 5, cu)
     for name, arr in (("q", q), ("k", k), ("v", v), ("cu", cu)):
         arr.tofile(str(tmp_path / f"{name}.bin"))
-    r = subprocess.run(["node", os.path.join(HERE, "js", "gpu.test.js"), str(tmp_path)],
+    r = subprocess.run(["node", "--expose-gc", os.path.join(HERE, "js", "gpu.test.js"), str(tmp_path)],
                        capture_output=True, text=True, timeout=180,
                        env=dict(os.environ, QATTN_EXPECT_GPU="1"))
     print(r.stdout, r.stderr[-2000:])
