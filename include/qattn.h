@@ -12,7 +12,7 @@
  *   CausalAttentionKernel.encode       ops.ts:344       | qattn_run_encode
  *   plan.destroy() of run.ownedBuffers model.ts:108-111 | qattn_run_destroy
  *   tiled flash attention shader       ops.ts:168-241   | kernel behind qattn_run_encode
- *   mask predicate + tile skip         ops.ts:205-220   | qattn_debug_mask (same device code)
+ *   mask predicate + tile skip         ops.ts:205-220   | qattn_debug_run_mask (executed), _debug_mask
  *   QKNormRopeKernel                   ops.ts:104-166   | qattn_qk_norm_rope
  *   RoPE table                         model.ts:76-83   | built inside qattn_qk_norm_rope
  *   last-token row of poolShader       ops.ts:357       | qattn_run_desc.o_last
@@ -184,6 +184,16 @@ int qattn_debug_mask(qattn_ctx* ctx, int32_t L, int32_t mask, int32_t prefix, in
 /* Host evaluation of the same iteration code (attn_common.h is compiled for host and device):
  * no device needed.  Same output layout as qattn_debug_mask. */
 int qattn_plan_mask(int32_t L, int32_t mask, int32_t prefix, int32_t window, uint32_t* host_bits);
+
+/* The retained-key set the attention kernel itself executes for a run (mask predicate
+ * ops.ts:205-209,219-220): runs the run's plan once through a variant of the attention kernel
+ * that also records, for every query head h, packed row t and key k of t's sequence, bit k%32
+ * of word host_bits[(h*T + t)*W + k/32] iff the masked score it computed for (t, k) is finite
+ * (T = tokens, W = *words_per_row = ceil(longest sequence / 32)).  The run's output buffers are
+ * written as by qattn_run_encode (o_last excepted).  host_bits NULL: only *words_per_row.
+ * Allocates a device buffer and synchronizes; a diagnostic, not for the hot path. */
+int qattn_debug_run_mask(qattn_run* run, uint32_t* host_bits, int64_t capacity_words,
+                         int32_t* words_per_row);
 
 /* ---- producer: QK RMSNorm + RoPE  (replaces QKNormRopeKernel, ops.ts:104-166) ------------- */
 /* In place on fp16 rows: for each token and each of `heads` 128-wide vectors at element

@@ -24,23 +24,6 @@
 #include "attn_common.h"
 
 namespace qattn {
-typedef _Float16 half_t;
-struct AttnParams {
-  const half_t* q;
-  const half_t* k;
-  const half_t* v;
-  half_t* o;
-  half_t* o_last;
-  uint32_t q_stride_b, k_stride_b, v_stride_b, o_stride_b;
-  const WorkItem* work;
-  const int32_t* slot_begin;
-  int32_t n_slots;
-  MaskSpec mask;
-  float scale_log2;
-  float* partials;          // split chunks' partial results (kPartialBytes each)
-  const WorkItem* splits;   // chunk 0 of each split item
-  int32_t n_splits;
-};
 hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream);
 hipError_t launch_attn_merge(const AttnParams& p, hipStream_t stream);
 hipError_t launch_debug_mask(int S, MaskSpec mask, uint32_t* bits, int words_per_row,
@@ -76,6 +59,7 @@ struct qattn_run {
   void* plan_dev = nullptr;  // work items by slot, then the slot offsets
   void* split_dev = nullptr; // the chunks' partial results (merged by a second kernel)
   int64_t v_offset = 0;
+  int32_t max_len = 0;  // longest sequence
   bool has_o_last = false;
   qattn_run_info info{};
 };
@@ -696,6 +680,7 @@ int qattn_run_create(qattn_ctx* ctx, const qattn_run_desc* d, qattn_run** out) {
   run->info = info;
   run->v_offset = d->v_offset;
   run->has_o_last = d->o_last != nullptr;
+  for (int32_t s = 0; s < d->nseq; ++s) run->max_len = std::max(run->max_len, d->cu_seqlens[s + 1] - d->cu_seqlens[s]);
   // One upload: the entries, the split items' chunk-0 entries, then the slot offsets (32-byte
   // entries keep the offsets aligned).
   const size_t items_bytes = plan.items.size() * sizeof(WorkItem);
@@ -847,6 +832,36 @@ int qattn_debug_mask(qattn_ctx* ctx, int32_t L, int32_t mask, int32_t prefix, in
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   (void)hipFree(dev);
   if (e != hipSuccess) return fail(ctx, QATTN_EHIP, "debug mask: %s", hipGetErrorString(e));
+  return QATTN_OK;
+}
+
+int qattn_debug_run_mask(qattn_run* run, uint32_t* host_bits, int64_t capacity_words,
+                         int32_t* words_per_row) {
+  if (!run) return fail(nullptr, QATTN_EINVAL, "run is NULL");
+  qattn_ctx* ctx = run->ctx;
+  const int32_t words = (run->max_len + 31) / 32;
+  if (words_per_row) *words_per_row = words;
+  if (!host_bits) return QATTN_OK;
+  const int64_t T = run->info.tokens;
+  const int64_t need = (int64_t)kQHeads * T * words;
+  if (capacity_words < need)
+    return fail(ctx, QATTN_EINVAL, "capacity %lld words < %lld (16 heads x %lld rows x %d)",
+                (long long)capacity_words, (long long)need, (long long)T, words);
+  if (need == 0) return QATTN_OK;
+  DeviceGuard g(ctx->device);
+  uint32_t* dev = nullptr;
+  HIP_TRY(ctx, hipMalloc(&dev, (size_t)need * sizeof(uint32_t)));
+  AttnParams p = run->params;
+  p.o_last = nullptr;
+  p.maskbits = dev;
+  p.mask_rows = (int32_t)T;
+  p.mask_words = words;
+  hipError_t e = hipMemsetAsync(dev, 0, (size_t)need * sizeof(uint32_t), ctx->stream);
+  if (e == hipSuccess) e = launch_attn_fwd(p, ctx->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(host_bits, dev, (size_t)need * sizeof(uint32_t), hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  (void)hipFree(dev);
+  if (e != hipSuccess) return fail(ctx, QATTN_EHIP, "run mask: %s", hipGetErrorString(e));
   return QATTN_OK;
 }
 

@@ -1,6 +1,7 @@
-// attn_common.h -- geometry, mask predicate and key-tile iterator shared by the attention
-// kernel, the debug-mask kernel and the host planner.  One definition of "which keys does a
-// query see" for every consumer, so the bit-exact mask check exercises the kernel's own code.
+// attn_common.h -- geometry, mask predicate, key-tile iterator and per-tile mask cases shared by
+// the attention kernel, the debug-mask kernel and the host planner.  The kernel selects its
+// element compares with tile_mask_case(); kept_keys_row() walks the same iteration with the same
+// case rules, and the kernel's MASKBITS variant reports what its executed compares kept.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -78,18 +79,44 @@ __host__ __device__ inline bool tile_full(int kb, int qa, int qb, int S, const M
   return ke < ps || qb - kb < ws;
 }
 
-// Element rule the kernel applies on tiles that are not tile_full, with ps = min(S, prefix) and
-// ws = min(S, window) precomputed.  For a query row q < S it equals retained(q, key, S, m):
-// key <= q implies key < S, and key + ws > q is key >= q - ws + 1.
+// Element rule on a tile that is not tile_full, with ps = min(S, prefix) and ws = min(S, window)
+// precomputed.  For a query row q < S it equals retained(q, key, S, m): key <= q implies
+// key < S, and key + ws > q is key >= q - ws + 1.
 __host__ __device__ inline bool keep_key(int q, int key, int ps, int ws, int kind) {
   return key <= q && (kind == 0 || key < ps || key >= q - ws + 1);
 }
 
+// The compares the attention kernel applies to a tile that is not tile_full for the wavefront
+// rows [wq0, wq1] (wq0 <= wq1 < S): the tile's position decides which conjuncts of keep_key can
+// fail for those rows, so most boundary tiles need one compare per key.
+enum TileMaskCase {
+  kDropAbove = 0,         // every key in the prefix or in every row's window: drop key > q
+  kDropBeforeWindow = 1,  // past the prefix, left of every row: drop key < q - ws + 1
+  kDropPastPrefix = 2,    // left of every row's window (the prefix's partial tile): drop key >= ps
+  kDropGeneral = 3        // straddles the prefix end and a window start: the full rule
+};
+__host__ __device__ inline int tile_mask_case(int kb, int wq0, int wq1, int ps, int ws, int kind) {
+  const int ke = kb + kTileK - 1;
+  if (kind == 0 || ke < ps || kb >= wq1 - ws + 1) return kDropAbove;
+  if (kb >= ps && ke <= wq0) return kDropBeforeWindow;
+  if (ke < wq0 - ws + 1) return kDropPastPrefix;
+  return kDropGeneral;
+}
+// The rule of each case for key `key` of row q -- what the kernel's compares keep.
+__host__ __device__ inline bool tile_case_keeps(int c, int q, int key, int ps, int ws) {
+  switch (c) {
+    case kDropAbove: return key <= q;
+    case kDropBeforeWindow: return key >= q - ws + 1;
+    case kDropPastPrefix: return key < ps;
+    default: return !(key > q || (key >= ps && key < q - ws + 1));
+  }
+}
+
 // Keys the attention kernel keeps for query row q of a sequence of length S, as a bitmask row
 // (word k/32, bit k%32; `row` pre-zeroed, `words` = ceil(S/32)).  Walks the kernel's own
-// iteration: every wavefront of a work item visits the work item's tile ranges (key_tiles over
-// its 64 rows); a tile that is tile_full for the wavefront's 32 rows keeps all its keys,
-// any other tile keeps the keys keep_key() admits.
+// iteration with the kernel's own per-tile decisions: every wavefront of a work item visits the
+// work item's tile ranges (key_tiles over its 64 rows); a tile that is tile_full for the
+// wavefront's 32 rows keeps all its keys, any other tile keeps what its tile_mask_case rule keeps.
 __host__ __device__ inline void kept_keys_row(int q, int S, const MaskSpec& m, uint32_t* row,
                                               int words) {
   const int blk_q0 = (q / kBlockQ) * kBlockQ;
@@ -102,11 +129,12 @@ __host__ __device__ inline void kept_keys_row(int q, int S, const MaskSpec& m, u
   for (int it = 0; it < tiles.count(); ++it) {
     const int kb = tiles.at(it) * kTileK;
     const bool full = tile_full(kb, wq0, wq1, S, m);
+    const int c = tile_mask_case(kb, wq0, wq1, ps, ws, m.kind);
     for (int wd = 0; wd < kTileK / 32; ++wd) {
       uint32_t word = 0;
       for (int b = 0; b < 32; ++b) {
         const int key = kb + 32 * wd + b;
-        if (full || keep_key(q, key, ps, ws, m.kind)) word |= 1u << b;
+        if (full || tile_case_keeps(c, q, key, ps, ws)) word |= 1u << b;
       }
       const int wi = kb / 32 + wd;
       if (wi < words) row[wi] = word;
@@ -130,5 +158,32 @@ struct WorkItem {
   int part;
 };
 constexpr int kMaxChunks = 8;  // chunks per split item (the merge kernel takes up to 8 per pass)
+
+typedef _Float16 half_t;
+
+// Arguments of one attention launch (host planner -> kernels).
+struct AttnParams {
+  const half_t* q;
+  const half_t* k;
+  const half_t* v;  // already offset by v_offset
+  half_t* o;
+  half_t* o_last;
+  uint32_t q_stride_b, k_stride_b, v_stride_b, o_stride_b;  // row strides in bytes (< 2^31)
+  const WorkItem* work;       // work items grouped by slot
+  const int32_t* slot_begin;  // slot b owns work[slot_begin[b] .. slot_begin[b+1])
+  int32_t n_slots;            // workgroups launched
+  MaskSpec mask;
+  float scale_log2;           // (1/sqrt(128)) * log2(e)
+  float* partials;            // split chunks' partial results (one record set per chunk)
+  const WorkItem* splits;     // chunk 0 of each split item, for the merge kernel
+  int32_t n_splits;
+  // Mask check only (qattn_debug_run_mask): when non-NULL the kernel also writes, for every
+  // query head h, packed row t and key k of t's sequence, bit k%32 of word
+  // maskbits[(h * mask_rows + t) * mask_words + k/32] iff the masked score it computed for
+  // (t, k) is finite, i.e. the key survived the compares it executed.
+  uint32_t* maskbits;
+  int32_t mask_rows;   // packed tokens T
+  int32_t mask_words;  // words per row: ceil(longest sequence / 32)
+};
 
 }  // namespace qattn

@@ -21,7 +21,8 @@
 //     j-1 in the same basic block as the softmax VALU work of tile j; the score / probability
 //     registers alternate between two sets by iteration parity (no copies); K and V are double
 //     buffered in LDS;
-//   * lazy rescaling: O and l are rescaled only when a row max grows by more than 2^8;
+//   * no per-tile row max: probabilities are taken against the entry's first-tile row max and
+//     O and l are rescaled only when a later tile's probabilities could leave fp16 range;
 //   * causal and prefix/local masks skip whole key tiles (key_tiles); element masks run only on
 //     tiles that straddle a boundary (tile_full).
 #include <hip/hip_runtime.h>
@@ -33,7 +34,6 @@
 
 namespace qattn {
 
-typedef _Float16 half_t;
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -45,24 +45,8 @@ typedef __attribute__((address_space(3))) s4 lds_s4_t;
 constexpr int kRowBytes = kHeadDim * 2;                      // 256 B per key row in LDS
 constexpr int kTileBytes = kTileK * kRowBytes;               // 16 KiB per K or V tile
 constexpr int kLoadsPerTile = kTileBytes / (kThreads * 16);  // 16 B per lane per load: 4
-constexpr float kRescaleThreshold = 8.0f;                    // log2 units
+constexpr float kLazyLimit = 32768.f;
 
-struct AttnParams {
-  const half_t* q;
-  const half_t* k;
-  const half_t* v;  // already offset by v_offset
-  half_t* o;
-  half_t* o_last;
-  uint32_t q_stride_b, k_stride_b, v_stride_b, o_stride_b;  // row strides in bytes (< 2^31)
-  const WorkItem* work;       // work items grouped by slot
-  const int32_t* slot_begin;  // slot b owns work[slot_begin[b] .. slot_begin[b+1])
-  int32_t n_slots;            // workgroups launched
-  MaskSpec mask;
-  float scale_log2;  // (1/sqrt(128)) * log2(e)
-  float* partials;          // split chunks' partial results (kPartialRecords x 64 lanes x 4 waves each)
-  const WorkItem* splits;   // chunk 0 of each split item, for the merge kernel
-  int32_t n_splits;
-};
 
 // Partial result of one chunk of a split item, per wavefront: 17 records of 64 lanes x float4
 // (records 0..15: the lane's 64 O^T accumulators, 16: m, l, 0, 0), so every access is a
@@ -157,8 +141,8 @@ __device__ inline void store_rows(const AttnParams& p, const f16x (&o)[4], float
 }
 
 // SPLIT: the plan has split items (partial-result path compiled in).  LAST: the run writes
-// o_last rows.
-template <bool SPLIT, bool LAST>
+// o_last rows.  MASKBITS: also report the kept keys (p.maskbits; the mask check only).
+template <bool SPLIT, bool LAST, bool MASKBITS = false>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   // K and V tiles, double buffered, 16 KiB each.  Four distinct objects (not offsets into one
   // array) with buffer choices fixed at compile time, so the compiler can see that the LDS-DMA
@@ -309,58 +293,79 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     }
   };
 
-  // Element mask of a boundary tile: the keys keep_key() drops become -inf.  With
-  // o = key_off(r) = key - kl (kl = kb + 4 hl), keep_key is
-  //   o <= d1  &&  (o < pe  ||  o >= d2),   d1 = q_pos - kl, pe = ps - kl, d2 = d1 - ws + 1,
-  // compares of compile-time offsets against per-lane thresholds.  The tile's position (uniform)
-  // decides which compares can fail, so most tiles need one compare + one select per element:
-  //   * every key in the prefix or in every row's window (all diagonal tiles, every tile of
-  //     the causal kind): only o <= d1;
-  //   * beyond the prefix and left of every row (a window-start tile): only o >= d2;
-  //   * left of every row's window (the prefix's last, partial tile): only o < pe.
+  // Element mask of a boundary tile: the keys its tile_mask_case rule drops become -inf.  With
+  // o = key_off(r) = key - kl (kl = kb + 4 hl), the rules are compares of compile-time offsets
+  // against per-lane thresholds (d1 = q_pos - kl, pe = ps - kl, d2 = d1 - ws + 1):
+  //   kDropAbove        drop o > d1                     (key > q)
+  //   kDropBeforeWindow drop o < d2                     (key < q - ws + 1)
+  //   kDropPastPrefix   drop o >= pe                    (key >= ps)
+  //   kDropGeneral      drop o > d1 || (o >= pe && o < d2)
+  // The case is uniform over the wavefront, so most boundary tiles cost one compare + one select
+  // per element.  kept_keys_row() (attn_common.h) evaluates the same cases on the host.
   auto apply_mask = [&](f16x (&s)[2], int kb) {
     const int kl = kb + 4 * hl;
     const int d1 = q_pos - kl;
-    const int ke = kb + kTileK - 1;
     auto drop_if = [&](auto pred) {
 #pragma unroll
       for (int r = 0; r < 32; ++r) s[r >> 4][r & 15] = pred(key_off(r)) ? -INFINITY : s[r >> 4][r & 15];
     };
-    if (mask.kind == 0 || ke < ps || kb >= wq1 - ws + 1) {
-      drop_if([&](int o) { return o > d1; });
-    } else if (kb >= ps && ke <= wq0) {
-      const int d2 = d1 - ws + 1;
-      drop_if([&](int o) { return o < d2; });
-    } else if (ke < wq0 - ws + 1) {
-      const int pe = ps - kl;
-      drop_if([&](int o) { return o >= pe; });
-    } else {
-      const int pe = ps - kl, d2 = d1 - ws + 1;
-      // bitwise, not short-circuit: one select per element instead of a branch
-      drop_if([&](int o) { return (o > d1) | ((o >= pe) & (o < d2)); });
+    switch (tile_mask_case(kb, wq0, wq1, ps, ws, mask.kind)) {
+      case kDropAbove:
+        drop_if([&](int o) { return o > d1; });
+        break;
+      case kDropBeforeWindow: {
+        const int d2 = d1 - ws + 1;
+        drop_if([&](int o) { return o < d2; });
+        break;
+      }
+      case kDropPastPrefix: {
+        const int pe = ps - kl;
+        drop_if([&](int o) { return o >= pe; });
+        break;
+      }
+      default: {
+        const int pe = ps - kl, d2 = d1 - ws + 1;
+        // bitwise, not short-circuit: one select per element instead of a branch
+        drop_if([&](int o) { return (o > d1) | ((o >= pe) & (o < d2)); });
+      }
     }
   };
 
-  // Online softmax of this lane's row over one tile's 64 scores -> fp16 P; returns whether the
-  // row max moved by more than the lazy-rescale threshold (then O must be scaled by alpha).
-  float m_run = -INFINITY;  // max (log2 domain) the probabilities are taken against
-  float l_run = 0.f;        // running sum of the fp16-rounded probabilities
-  auto softmax = [&](const f16x (&s)[2], h8 (&pf)[4], float& alpha) {
-    float mx = fmaxf(fmaxf(s[0][0], s[0][1]), s[0][2]);
+  // Mask check: which keys of this tile survived for this lane's row (finite masked score).
+  // Lane half hl holds keys kb + 4hl + key_off(r); one permlane32 swap merges the two halves,
+  // leaving the word of keys kb..kb+31 in the low half-wave and kb+32..kb+63 in the high one.
+  // (Extra stores: the pipeline's vmcnt waits only become stricter.)
+  auto record_mask = [&](const f16x (&s)[2], int kb) {
+    uint32_t w0 = 0, w1 = 0;
 #pragma unroll
-    for (int r = 3; r < 31; r += 2) mx = fmaxf(fmaxf(mx, s[r >> 4][r & 15]), s[(r + 1) >> 4][(r + 1) & 15]);
-    mx = fmaxf(mx, s[1][15]);
-    mx = pair_max(mx);
-    const float m_cand = fmaxf(m_run, mx * c);
-    const bool need = m_cand > m_run + kRescaleThreshold;
-    const float m_next = need ? m_cand : m_run;
-    const float m_use = m_next == -INFINITY ? 0.f : m_next;
-    alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    // P in fp16 feeds the PV MFMA; the row sum adds those same rounded values (exactly, via
-    // v_dot2 against 1.0), so O is an exact weighted mean of V and the fp16 rounding of P only
-    // perturbs the weights.
-    float psum = 0.f;
-    const h2 ones = {(half_t)1.0f, (half_t)1.0f};
+    for (int r = 0; r < 16; ++r) {
+      const int bit = 8 * (r >> 2) + (r & 3) + 4 * hl;
+      w0 |= (s[0][r] != -INFINITY ? 1u : 0u) << bit;
+      w1 |= (s[1][r] != -INFINITY ? 1u : 0u) << bit;
+    }
+    const auto x = __builtin_amdgcn_permlane32_swap(w0, w1, false, false);
+    const int word = kb / 32 + hl;
+    if (q_pos < S && word < (S + 31) / 32) {
+      const int head = kvh * kGroup + head_in_group;
+      p.maskbits[((size_t)head * p.mask_rows + seq_start + q_pos) * p.mask_words + word] = x[0] | x[1];
+    }
+  };
+
+  // Online softmax.  The probabilities of a row are taken against a reference m_run (log2
+  // domain): P = f16(2^(s c - m_run)), O = sum P V, l = sum P.  m_run is the row max of the
+  // entry's first tile and moves only when a later tile's probabilities could leave fp16 range:
+  // no per-tile max, no per-tile rescale.  A lane whose half-row sum of one tile exceeds
+  // kLazyLimit (2^15; each P is then <= 2^15 < 65504, the fp16 maximum) -- or is inf / NaN
+  // (m_run still -inf: every key so far masked) -- sends the wavefront through the full update:
+  // tile max, new reference, O and l scaled by alpha, P recomputed.  After the first tile with
+  // a key, l >= 1 (the max key has P = 1), so small P values lose nothing relative to l.
+  float m_run = -INFINITY;  // reference (log2 domain) the probabilities are taken against
+  float l_run = 0.f;        // running sum of the fp16-rounded probabilities
+  // P in fp16 feeds the PV MFMA; the row sum adds those same rounded values (exactly: each f16
+  // is widened inside v_fma_mix_f32), so O is an exact weighted mean of V and the fp16 rounding
+  // of P only perturbs the weights.
+  auto probs = [&](const f16x (&s)[2], h8 (&pf)[4], float m_use) {
+    float ps0 = 0.f, ps1 = 0.f;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
 #pragma unroll
@@ -368,21 +373,45 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
         const int r = 8 * t + j;
         pf[t][j] = (half_t)__builtin_amdgcn_exp2f(fmaf(s[r >> 4][r & 15], c, -m_use));
       }
+      typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+      const u4 pairs = __builtin_bit_cast(u4, pf[t]);
 #pragma unroll
-      for (int j = 0; j < 8; j += 2) {
-        const h2 pair = {pf[t][j], pf[t][j + 1]};
-        psum = __builtin_amdgcn_fdot2(pair, ones, psum, false);
+      for (int j = 0; j < 4; ++j) {
+        float& ps = (j & 1) ? ps1 : ps0;
+        asm("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel_hi:[1,0,0]\n\t"
+            "v_fma_mix_f32 %0, %1, 1.0, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+            : "+v"(ps)
+            : "v"(pairs[j]));
       }
     }
-    m_run = m_next;
-    l_run = l_run * alpha + psum;
-    return need;
+    return ps0 + ps1;
   };
-  auto rescale = [&](bool need, float alpha) {
-    if (__builtin_amdgcn_ballot_w64(need) != 0) {
+  auto tile_max = [&](const f16x (&s)[2]) {
+    float mx = fmaxf(fmaxf(s[0][0], s[0][1]), s[0][2]);
+#pragma unroll
+    for (int r = 3; r < 31; r += 2) mx = fmaxf(fmaxf(mx, s[r >> 4][r & 15]), s[(r + 1) >> 4][(r + 1) & 15]);
+    mx = fmaxf(mx, s[1][15]);
+    return pair_max(mx);
+  };
+  // The entry's first tile: O = 0, l = 0; the reference is this tile's row max.
+  auto softmax_first = [&](const f16x (&s)[2], h8 (&pf)[4]) {
+    m_run = tile_max(s) * c;
+    l_run = probs(s, pf, m_run == -INFINITY ? 0.f : m_run);
+  };
+  // Later tiles: the fast path, or the full update for the whole wavefront when any lane needs it.
+  auto softmax_next = [&](const f16x (&s)[2], h8 (&pf)[4]) {
+    float psum = probs(s, pf, m_run);
+    if (__builtin_amdgcn_ballot_w64(!(psum <= kLazyLimit)) != 0) {
+      const float m_new = fmaxf(m_run, tile_max(s) * c);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);  // 0 while m_run is -inf
+      psum = probs(s, pf, m_use);
 #pragma unroll
       for (int db = 0; db < 4; ++db) o[db] *= alpha;
+      l_run *= alpha;
+      m_run = m_new;
     }
+    l_run += psum;
   };
 
   // Two register sets for scores / probabilities, alternating by iteration parity.
@@ -425,6 +454,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     // the waits below stay exact.
     if (last) start_loads(work(next_index));
     if (!tile_full(kb, wq0, wq1, S, mask)) apply_mask(s_cur, kb);
+    if constexpr (MASKBITS) record_mask(s_cur, kb);
     if (!last) {
       qk(knext, s_nxt, [&](int st) {
         if (st < kLoadsPerTile) {
@@ -440,12 +470,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
       s_nxt[1] = f16x{};
     }
     if (with_pv) pv(vprev, p_prev);
-    float alpha;
-    const bool need = softmax(s_cur, p_cur, alpha);
-    // Keep P(it) and the row sum computed here, beside the MFMAs above: without this use the
-    // compiler sinks the exponentials below the rescale branch, where no MFMA work overlaps them.
-    asm volatile("" ::"v"(p_cur[0]), "v"(p_cur[1]), "v"(p_cur[2]), "v"(p_cur[3]), "v"(l_run));
-    rescale(need, alpha);
+    if (with_pv)
+      softmax_next(s_cur, p_cur);
+    else
+      softmax_first(s_cur, p_cur);
     if (last) {
       // The item's last PV.  V(it) has landed once at most the next item's kPrefetchOps loads
       // are in flight.  (Here, not after the loop, so the V buffer stays a compile-time choice
@@ -622,6 +650,11 @@ hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream) {
   // Plans without split items run the variant without the partial-result path (fewer live
   // registers in the tile loop).
   const dim3 grid(p.n_slots), block(kThreads);
+  if (p.maskbits) {
+    if (p.n_splits > 0) hipLaunchKernelGGL((attn_fwd_kernel<true, false, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((attn_fwd_kernel<false, false, true>), grid, block, 0, stream, p);
+    return hipGetLastError();
+  }
   if (p.n_splits > 0) {
     if (p.o_last) hipLaunchKernelGGL((attn_fwd_kernel<true, true>), grid, block, 0, stream, p);
     else hipLaunchKernelGGL((attn_fwd_kernel<true, false>), grid, block, 0, stream, p);

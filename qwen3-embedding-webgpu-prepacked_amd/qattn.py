@@ -95,6 +95,7 @@ def lib():
         "qattn_prefill": (ctypes.c_int, [vp, ctypes.POINTER(RunDesc), vp]),
         "qattn_debug_mask": (ctypes.c_int, [vp, i32, i32, i32, i32, vp]),
         "qattn_plan_mask": (ctypes.c_int, [i32, i32, i32, i32, vp]),
+        "qattn_debug_run_mask": (ctypes.c_int, [vp, vp, i64, ctypes.POINTER(i32)]),
         "qattn_qk_norm_rope": (ctypes.c_int, [vp, vp, i64, i64, i32, vp, i32, vp,
                                               ctypes.c_double, ctypes.c_double, vp]),
         "qattn_pool_last_l2": (ctypes.c_int, [vp, vp, i64, i32, vp, i32, vp, i64, vp]),
@@ -220,6 +221,16 @@ class Run:
         i = RunInfo()
         _check(lib().qattn_run_get_info(self.handle, ctypes.byref(i)), self.ctx.handle)
         return i
+
+    def mask_bits(self):
+        """Keys the kernel kept (qattn_debug_run_mask): uint32 [16 heads, tokens, words]."""
+        words = ctypes.c_int32()
+        _check(lib().qattn_debug_run_mask(self.handle, None, 0, ctypes.byref(words)), self.ctx.handle)
+        T = self.info().tokens
+        out = np.zeros((HQ, T, words.value), dtype=np.uint32)
+        _check(lib().qattn_debug_run_mask(self.handle, _np_ptr(out) if out.size else None, out.size,
+                                          ctypes.byref(words)), self.ctx.handle)
+        return out
 
     def destroy(self):
         if self.handle:

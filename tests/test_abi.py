@@ -240,6 +240,20 @@ def test_kernel_key_iteration_other_masks(qattn, oracle, L, mask, P, W):
     assert np.array_equal(qattn.plan_mask(L, mask, P, W), oracle.mask_bits(L, mask, P, W))
 
 
+def test_kernel_mask_cases_sweep(qattn, oracle):
+    # Every tile-mask case (tile_mask_case / tile_case_keeps, the compares the kernel executes)
+    # over a grid of lengths, prefixes and windows around the tile and wavefront boundaries.
+    n = 0
+    for P in (0, 1, 5, 31, 32, 33, 63, 64, 65, 100, 176):
+        for W in (0, 1, 2, 31, 32, 33, 63, 64, 65, 97, 432):
+            if P == 0 and W == 0:
+                continue
+            for L in (1, 33, 64, 65, 129, 191, 257, 300):
+                assert np.array_equal(qattn.plan_mask(L, 1, P, W), oracle.mask_bits(L, 1, P, W)), (L, P, W)
+                n += 1
+    assert n == 960
+
+
 def test_q4_compact_bytes(qattn, oracle):
     f = qattn.lib().qattn_q4_compact_bytes
     assert f(1024, 4096) == 128 * 32 * 32 * 20

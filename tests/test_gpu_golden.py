@@ -49,18 +49,26 @@ def compare_golden(got_bits, want_bits, label):
     assert cos.min() >= MIN_COS, (label, cos.min())
 
 
-@pytest.mark.parametrize("config,flags", [(0, 0), (1, 0), (2, 0), (3, 0), (3, 1), (4, 0), (4, 1)])
-def test_config_rows_match_golden(ctx, qattn, oracle, golden, hashes, config, flags):
+# (config, flags, mask, o_last).  Configs 0-2 never exceed 608 tokens, where the prefix/local
+# mask equals full causal, so both mask kinds must reproduce the same golden rows; (2, 0, 0, False)
+# is exactly the launch bench.py times for its 16 x 500 line (causal kind, no flags, no o_last).
+@pytest.mark.parametrize("config,flags,mask,o_last", [
+    (0, 0, 1, True), (1, 0, 1, True), (2, 0, 1, True), (3, 0, 1, True), (3, 1, 1, True),
+    (4, 0, 1, True), (4, 1, 1, True), (2, 0, 0, False), (1, 0, 0, False)])
+def test_config_rows_match_golden(ctx, qattn, oracle, golden, hashes, config, flags, mask, o_last):
     cu = golden[f"cfg{config}_cu"].astype(np.int32)
     rows = golden[f"cfg{config}_rows"]
-    print(f"golden cfg{config} flags {flags}: lengths {np.diff(cu).tolist()[:4]}... rows {len(rows)}",
-          flush=True)
+    print(f"golden cfg{config} flags {flags} mask {mask} o_last {o_last}: lengths "
+          f"{np.diff(cu).tolist()[:4]}... rows {len(rows)}", flush=True)
     q, k, v = oracle.gen_qkv(config, 0, cu)
     for name, a in (("q", q), ("k", k), ("v", v)):
         assert sha(a) == hashes[f"cfg{config}/layer0/{name}"], name
-    case = Case(ctx, qattn, q, k, v, cu, o_last=True, flags=flags)
+    case = Case(ctx, qattn, q, k, v, cu, mask=mask, o_last=o_last, flags=flags)
     got = case.run()
-    compare_golden(got[rows], golden[f"cfg{config}_out"], f"cfg{config} flags {flags}")
+    compare_golden(got[rows], golden[f"cfg{config}_out"], f"cfg{config} flags {flags} mask {mask}")
+    if not o_last:
+        case.free()
+        return
     last = case.last()
     ends = cu[1:] - 1
     # o_last holds exactly the last output row of each sequence.

@@ -101,6 +101,52 @@ def test_debug_mask_other_masks(ctx, oracle, L, mask, P, W):
     assert np.array_equal(ctx.debug_mask(L, mask, P, W), oracle.mask_bits(L, mask, P, W))
 
 
+# The retained-key set the attention kernel itself executes (qattn_debug_run_mask: the real
+# launch, with its planner, tile skipping, per-tile mask cases and split-K chunks, reporting which
+# masked scores came out finite), bit for bit against the reference predicate, for every query
+# head of every sequence.  (lengths, mask, prefix, window, flags).
+_REF_LENGTHS = [1, 16, 63, 64, 65, 175, 176, 177, 431, 432, 433, 607, 608, 609, 1500, 5000]
+EXEC_MASK_CASES = (
+    [([L], 1, 176, 432, 0) for L in _REF_LENGTHS]
+    + [([L], 0, 0, 0, 0) for L in (1, 64, 65, 500, 609, 1500)]
+    + [([333], 1, 7, 50, 0), ([300], 1, 0, 33, 0), ([700], 1, 1, 1, 0), ([1000], 1, 64, 64, 0),
+       ([900], 1, 200, 0, 0), ([777], 1, 0, 500, 0)]
+    + [([500] * 16, 0, 0, 0, 0),            # the benched 16 x 500 launch
+       ([5000], 1, 176, 432, 1),            # batch-invariant plan (no split-K)
+       ([5000] * 4, 1, 176, 432, 0),        # config 4
+       ([1, 609, 64, 177, 1500, 2], 1, 176, 432, 0)])
+
+
+@pytest.mark.parametrize("lengths,mask,P,W,flags", EXEC_MASK_CASES,
+                         ids=[f"{len(c[0])}x{c[0][0]}-m{c[1]}-{c[2]}-{c[3]}-f{c[4]}" for c in EXEC_MASK_CASES])
+def test_executed_mask_bit_exact(ctx, qattn, oracle, lengths, mask, P, W, flags):
+    cu = cu_of(lengths)
+    T = int(cu[-1])
+    bq, bk, bv, bo = ctx.alloc(T * 4096), ctx.alloc(T * 2048), ctx.alloc(T * 2048), ctx.alloc(T * 4096)
+    ctx.gen_qkv(1, 0, cu, bq.ptr, bk.ptr, bv.ptr)
+    run = ctx.run(qattn.make_desc(bq.ptr, bk.ptr, bv.ptr, bo.ptr, cu, mask, P, W, flags=flags))
+    info = run.info()
+    print(f"executed mask {lengths[:3]}{'...' if len(lengths) > 3 else ''} mask {mask} P {P} W {W} "
+          f"flags {flags}: {info.work_items} items, {info.split_items} split", flush=True)
+    bits = run.mask_bits()
+    assert bits.shape[:2] == (HQ, T)
+    cache = {}
+    for s, L in enumerate(lengths):
+        if L not in cache:
+            cache[L] = oracle.mask_bits(L, mask, P, W)
+        want = cache[L]
+        w = want.shape[1]
+        got = bits[:, cu[s]:cu[s + 1], :]
+        assert np.array_equal(got[:, :, :w], np.broadcast_to(want, (HQ,) + want.shape)), (s, L)
+        assert not got[:, :, w:].any(), (s, L)
+        # the retained-pair count, from the bits, equals the closed form
+        assert int(np.unpackbits(got[0].view(np.uint8)).sum()) == oracle.mask_pairs(L, mask, P, W)
+    run.destroy()
+    for b in (bq, bk, bv, bo):
+        b.free()
+
+
+
 def ulp_distance(a, b):
     """Distance in units of the last place between fp16 bit patterns of the same sign."""
     a = a.astype(np.int32)
