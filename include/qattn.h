@@ -167,6 +167,17 @@ int qattn_plan_slots(const qattn_run_desc* desc, int32_t max_slots, int32_t* slo
 /* One-shot: create, encode, wait for completion, destroy. */
 int qattn_prefill(qattn_ctx* ctx, const qattn_run_desc* desc, qattn_stream_t stream);
 
+/* No counterpart in the reference.  For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): qattn_prefill with no
+ * device allocation or free.  The plan is always batch-invariant (no split-K), so the output is
+ * bitwise that of qattn_prefill with QATTN_FLAG_BATCH_INVARIANT set.  Its work list goes to a
+ * fixed 1 MiB array in the library's device image (one per GPU, kept until the process ends):
+ * launches of more than about 32000 work entries (64-query blocks x 8 KV heads, roughly 250k
+ * tokens) are rejected with QATTN_EINVAL.  Every call on one GPU uses that GPU's array, so calls
+ * that overlap on one GPU (other threads or streams) race; each call waits for its stream before
+ * returning.  Host-side planning uses host memory only. */
+int qattn_prefill_static(qattn_ctx* ctx, const qattn_run_desc* desc, qattn_stream_t stream);
+
 /* ---- mask check  (same device predicate and key-tile iterator as the attention kernel) ---- */
 /* Diagnostic, no counterpart in the reference: the XCD (hardware XCC_ID) that each of n
  * workgroups of a launch shaped like the attention kernel's runs on.  The planner keeps each KV

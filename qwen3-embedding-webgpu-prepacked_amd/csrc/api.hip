@@ -45,10 +45,22 @@ hipError_t launch_qk_norm_rope(half_t* x, int64_t row_stride, int64_t col0, int 
 
 using namespace qattn;
 
+// Work-list storage of qattn_prefill_static, the entry point that allocates no device memory:
+// a fixed array in the library's own device image, one copy per GPU, held until the process
+// ends.  Host code never uses its name as an address (that would be a host stand-in): each
+// context resolves the device address once, with its device current, in qattn_create, and passes
+// that pointer on.  1 MiB holds the work list (32-byte entries) and the slot offsets of launches
+// of up to about 32000 entries -- 64-query blocks x 8 KV heads, roughly 250k tokens.
+namespace {
+constexpr size_t kScratchBytes = (size_t)1 << 20;
+}
+static __device__ __align__(256) char scratch[kScratchBytes];
+
 struct qattn_ctx {
   int device = 0;
   int cu_count = 0;
   hipStream_t stream = nullptr;
+  void* scratch = nullptr;  // this device's copy of `scratch` (qattn_prefill_static)
   std::string last_error;
   std::mutex mu;
 };
@@ -210,6 +222,12 @@ int qattn_create(int device, qattn_ctx** out) {
   if (e != hipSuccess) {
     delete ctx;
     return fail(nullptr, QATTN_EHIP, "hipStreamCreate: %s", hipGetErrorString(e));
+  }
+  e = hipGetSymbolAddress(&ctx->scratch, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !ctx->scratch) {
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return fail(nullptr, QATTN_EHIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
   }
   *out = ctx;
   return QATTN_OK;
@@ -628,6 +646,28 @@ int plan_work(qattn_ctx* ctx, const qattn_run_desc* d, int max_slots, Plan* out,
   return QATTN_OK;
 }
 
+// Launch arguments of a validated description whose work list sits at `plan` (entries, then the
+// split items' chunk-0 entries, then the slot offsets).
+void fill_params(AttnParams* p, const qattn_run_desc* d, const MaskSpec& mask, int32_t slots, const void* plan,
+                 size_t items_bytes, size_t heads_bytes) {
+  p->q = static_cast<const half_t*>(d->q);
+  p->k = static_cast<const half_t*>(d->k);
+  p->v = static_cast<const half_t*>(d->v) + d->v_offset;
+  p->o = static_cast<half_t*>(d->o);
+  p->o_last = static_cast<half_t*>(d->o_last);
+  // Byte strides fit 32 bits: (L + 64) * stride * 2 < 2^31 is validated for every sequence.
+  p->q_stride_b = (uint32_t)(d->q_row_stride * 2);
+  p->k_stride_b = (uint32_t)(d->k_row_stride * 2);
+  p->v_stride_b = (uint32_t)(d->v_row_stride * 2);
+  p->o_stride_b = (uint32_t)(d->o_row_stride * 2);
+  p->work = static_cast<const WorkItem*>(plan);
+  p->splits = reinterpret_cast<const WorkItem*>(static_cast<const char*>(plan) + items_bytes);
+  p->slot_begin = reinterpret_cast<const int32_t*>(static_cast<const char*>(plan) + items_bytes + heads_bytes);
+  p->n_slots = slots;
+  p->mask = mask;
+  p->scale_log2 = (float)(1.4426950408889634 / std::sqrt(128.0));
+}
+
 }  // namespace
 
 extern "C" {
@@ -716,24 +756,9 @@ int qattn_run_create(qattn_ctx* ctx, const qattn_run_desc* d, qattn_run** out) {
     }
   }
   AttnParams& p = run->params;
+  fill_params(&p, d, mask, info.slots, run->plan_dev, items_bytes, heads_bytes);
   p.partials = static_cast<float*>(run->split_dev);
-  p.splits = reinterpret_cast<const WorkItem*>(static_cast<const char*>(run->plan_dev) + items_bytes);
   p.n_splits = plan.splits;
-  p.q = static_cast<const half_t*>(d->q);
-  p.k = static_cast<const half_t*>(d->k);
-  p.v = static_cast<const half_t*>(d->v) + d->v_offset;
-  p.o = static_cast<half_t*>(d->o);
-  p.o_last = static_cast<half_t*>(d->o_last);
-  // Byte strides fit 32 bits: (L + 64) * stride * 2 < 2^31 is validated for every sequence.
-  p.q_stride_b = (uint32_t)(d->q_row_stride * 2);
-  p.k_stride_b = (uint32_t)(d->k_row_stride * 2);
-  p.v_stride_b = (uint32_t)(d->v_row_stride * 2);
-  p.o_stride_b = (uint32_t)(d->o_row_stride * 2);
-  p.work = static_cast<const WorkItem*>(run->plan_dev);
-  p.slot_begin = reinterpret_cast<const int32_t*>(static_cast<const char*>(run->plan_dev) + items_bytes + heads_bytes);
-  p.n_slots = info.slots;
-  p.mask = mask;
-  p.scale_log2 = (float)(1.4426950408889634 / std::sqrt(128.0));
   *out = run;
   return QATTN_OK;
 }
@@ -793,6 +818,39 @@ int qattn_prefill(qattn_ctx* ctx, const qattn_run_desc* desc, qattn_stream_t str
   }
   qattn_run_destroy(run);
   return rc;
+}
+
+int qattn_prefill_static(qattn_ctx* ctx, const qattn_run_desc* desc, qattn_stream_t stream) {
+  if (!ctx) return fail(nullptr, QATTN_EINVAL, "ctx is NULL");
+  if (!desc) return fail(ctx, QATTN_EINVAL, "desc is NULL");
+  if (!ctx->scratch) return fail(ctx, QATTN_EHIP, "the static work list has no device address");
+  // Batch-invariant plan: no split-K, so no partial results -- the work list is all it stores.
+  qattn_run_desc d = *desc;
+  d.flags |= QATTN_FLAG_BATCH_INVARIANT;
+  Plan plan;
+  qattn_run_info info{};
+  MaskSpec mask{};
+  int rc = plan_work(ctx, &d, std::max(1, ctx->cu_count) * kBlocksPerCU, &plan, &info, &mask);
+  if (rc) return rc;
+  const size_t items_bytes = plan.items.size() * sizeof(WorkItem);
+  const size_t slots_bytes = plan.slot_begin.size() * sizeof(int32_t);
+  if (items_bytes + slots_bytes > kScratchBytes)
+    return fail(ctx, QATTN_EINVAL,
+                "%zu work entries exceed the static work list (%zu bytes, about %zu entries); use "
+                "qattn_prefill or qattn_run_create",
+                plan.items.size(), kScratchBytes, (kScratchBytes - 513 * sizeof(int32_t)) / sizeof(WorkItem));
+  std::vector<char> host(items_bytes + slots_bytes);
+  if (items_bytes) std::memcpy(host.data(), plan.items.data(), items_bytes);
+  std::memcpy(host.data() + items_bytes, plan.slot_begin.data(), slots_bytes);
+  AttnParams p{};
+  fill_params(&p, &d, mask, info.slots, ctx->scratch, items_bytes, 0);
+  DeviceGuard g(ctx->device);
+  hipStream_t st = pick_stream(ctx, stream);
+  HIP_TRY(ctx, hipMemcpyAsync(ctx->scratch, host.data(), host.size(), hipMemcpyHostToDevice, st));
+  HIP_TRY(ctx, launch_attn_fwd(p, st));
+  // Also keeps `host` alive until the copy has run, and the work list until the kernel is done.
+  HIP_TRY(ctx, hipStreamSynchronize(st));
+  return QATTN_OK;
 }
 
 // ---- mask check -------------------------------------------------------------------------------

@@ -93,6 +93,7 @@ def lib():
         "qattn_plan_slots": (ctypes.c_int, [ctypes.POINTER(RunDesc), i32, vp, i32, ctypes.POINTER(i32)]),
         "qattn_debug_xcd_map": (ctypes.c_int, [vp, i32, vp]),
         "qattn_prefill": (ctypes.c_int, [vp, ctypes.POINTER(RunDesc), vp]),
+        "qattn_prefill_static": (ctypes.c_int, [vp, ctypes.POINTER(RunDesc), vp]),
         "qattn_debug_mask": (ctypes.c_int, [vp, i32, i32, i32, i32, vp]),
         "qattn_plan_mask": (ctypes.c_int, [i32, i32, i32, i32, vp]),
         "qattn_debug_run_mask": (ctypes.c_int, [vp, vp, i64, ctypes.POINTER(i32)]),
@@ -302,6 +303,10 @@ class Context:
 
     def prefill(self, desc, stream=None):
         _check(lib().qattn_prefill(self.handle, ctypes.byref(desc), stream), self.handle)
+
+    def prefill_static(self, desc, stream=None):
+        """qattn_prefill_static: the same launch with no device allocation (batch-invariant plan)."""
+        _check(lib().qattn_prefill_static(self.handle, ctypes.byref(desc), stream), self.handle)
 
     def debug_mask(self, L, mask=MASK_PREFIX_LOCAL, prefix=176, window=432):
         words = (L + 31) // 32
