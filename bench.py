@@ -8,18 +8,27 @@ of independent seeded Q/K/V resident in HBM:
 Every launch is one layer's attention through the C ABI (qattn_run_encode), exactly what the
 Node engine issues.  Timing: HIP events on the launch stream around exactly K steps, with a
 device synchronize on both sides.  A second pass brackets every launch with its own events to
-get the kernel's average duration for the roofline figure.
+get each workload's average kernel duration -- for the headline workloads and, reported beside
+them in config.breakdown, for the other BASELINE configs (0: 1 x 50, 1: 16 ragged 10..150,
+3: 1 x 1500 sparse, 4: 4 x 5000 sparse with last-token rows).
 
-cpu_baseline: the reference's tiled algorithm restated on the CPU (oracle/, f16-faithful, the
-"port"), timed on a bounded sample of the same workload on this host's cores.
+cpu_baseline: the reference's tiled kernel (src/webgpu/ops.ts:168-241) restated in JavaScript
+(oracle/tiled16.js, f16 rounding points as the WGSL) and run under Node on this host's cores,
+on a bounded sample of the same two workloads, once on one thread and once on worker threads;
+its output is first checked bit for bit against the C restatement on config 0.  The C port's
+own OpenMP timing is reported beside it as a cross-check.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload both|full|sparse|cfg3|cfg4]
 """
 import argparse
+import hashlib
 import importlib.util
 import json
 import os
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
 
 import numpy as np
@@ -29,16 +38,44 @@ PKG = os.path.join(REPO, "qwen3-embedding-webgpu-prepacked_amd")
 LAYERS = 28
 PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16/bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+CPU_THREADS_MAX = 16        # a GPU box's CPU share
+
+
+def mix64(z):
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9 & 0xFFFFFFFFFFFFFFFF
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EB & 0xFFFFFFFFFFFFFFFF
+    return z ^ (z >> 31)
+
+
+def config_seed(config, layer, tensor):
+    return 0x51574E3300000000 | (config & 0xFF) << 16 | (layer & 0xFF) << 8 | (tensor & 0xFF)
+
+
+def config1_lengths():
+    """16 lengths uniform in 10..150 from the SplitMix64 stream of tensor 3
+    (the generator qattn_gen_qkv seeds Q/K/V from: seed + (i + 1) * golden ratio, finalised)."""
+    s = config_seed(1, 0, 3)
+    return [10 + (mix64((s + (i + 1) * 0x9E3779B97F4A7C15) & 0xFFFFFFFFFFFFFFFF) >> 33) % 141
+            for i in range(16)]
+
 
 WORKLOADS = {
-    # name: (config id for seeds, lengths, mask kind, description)
-    "full": (2, [500] * 16, 0, "16x500 full causal"),
-    "sparse": (5, [5000], 1, "1x5000 sparse (176 prefix + 432 window)"),
-    "cfg3": (3, [1500], 1, "1x1500 sparse (176 prefix + 432 window)"),
-    "cfg4": (4, [5000] * 4, 1, "4x5000 sparse (176 prefix + 432 window) + last rows"),
+    # name: (config id for seeds, lengths, mask kind, o_last, description)
+    "full": (2, [500] * 16, 0, False, "16x500 full causal"),
+    "sparse": (5, [5000], 1, False, "1x5000 sparse (176 prefix + 432 window)"),
+    "cfg0": (0, [50], 1, False, "cfg0 1x50 causal"),
+    "cfg1": (1, None, 1, False, "cfg1 16 ragged 10..150 causal"),
+    "cfg3": (3, [1500], 1, False, "cfg3 1x1500 sparse (176 prefix + 432 window)"),
+    "cfg4": (4, [5000] * 4, 1, True, "cfg4 4x5000 sparse (176 prefix + 432 window) + last rows"),
 }
 SETS = {"both": ["full", "sparse"], "full": ["full"], "sparse": ["sparse"], "cfg3": ["cfg3"],
         "cfg4": ["cfg4"]}
+EXTRA = ["cfg0", "cfg1", "cfg3", "cfg4"]  # reported in the breakdown of the default run
+
+
+def lengths_of(name):
+    lengths = WORKLOADS[name][1]
+    return config1_lengths() if lengths is None else lengths
 
 
 def log(*a):
@@ -58,18 +95,18 @@ class Workload:
 
     def __init__(self, ctx, q, name):
         self.name = name
-        cfg, lengths, mask, desc = WORKLOADS[name]
+        cfg, _, mask, o_last, desc = WORKLOADS[name]
         self.desc_text = desc
-        self.lengths = lengths
-        self.cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+        self.lengths = lengths_of(name)
+        self.cu = np.concatenate([[0], np.cumsum(self.lengths)]).astype(np.int32)
         T = int(self.cu[-1])
         self.tokens = T
-        nseq = len(lengths)
+        nseq = len(self.lengths)
         self.bufs, self.runs = [], []
         for layer in range(LAYERS):
             bq, bk, bv = ctx.alloc(T * 4096), ctx.alloc(T * 2048), ctx.alloc(T * 2048)
             bo = ctx.alloc(T * 4096)
-            bl = ctx.alloc(nseq * 4096) if name == "cfg4" else None
+            bl = ctx.alloc(nseq * 4096) if o_last else None
             ctx.gen_qkv(cfg, layer, self.cu, bq.ptr, bk.ptr, bv.ptr)
             d = q.make_desc(bq.ptr, bk.ptr, bv.ptr, bo.ptr, self.cu, mask=mask,
                             o_last=bl.ptr if bl else None)
@@ -89,52 +126,131 @@ class Workload:
             b.free()
 
 
+# ---- CPU baseline (the checker's restatements; never the measured GPU path) --------------------
+
+def visited_key_tiles(L, kind, prefix=176, window=432):
+    """16-key tiles the reference kernel visits per 16-query tile gx (its loop and skip,
+    ops.ts:205-209): the work measure the sample is scaled by."""
+    out = []
+    ps, ws = min(L, prefix), min(L, window)
+    for gx in range((L + 15) // 16):
+        limit = min(L, (gx + 1) * 16)
+        start = gx * 16 + 1 - ws if gx * 16 + 1 > ws else 0
+        n = 0
+        for kb in range(0, limit, 16):
+            if kind == 1 and kb >= ps and kb + 15 < start:
+                continue
+            n += 1
+        out.append(n)
+    return out
+
+
+def node_samples(name, per_stratum):
+    """Sample of (sequence, query tile, head) groups of one workload's layer 0, and the factor that
+    scales its visited-tile count to the whole layer's.  16 x 500: every 2nd query tile of
+    sequence 0 (all sequences are alike), `per_stratum` heads each; 1 x 5000: every 16th query
+    tile, `per_stratum` heads each (heads cost the same).  A run on N threads takes N heads per
+    query tile, so its wall time stays near the one-thread run's."""
+    cfg, _, kind, _, _ = WORKLOADS[name]
+    lengths = lengths_of(name)
+    L = lengths[0]
+    vt = visited_key_tiles(L, kind)
+    step = 2 if name == "full" else 16
+    sample, sampled = [], 0
+    for gx in range(0, len(vt), step):
+        for j in range(per_stratum):
+            sample.append([0, gx, (gx // step * per_stratum + j) % 16])
+            sampled += vt[gx]
+    total = sum(vt) * 16 * len(lengths)
+    return sample, total / sampled, kind
+
+
 def cpu_baseline(selected):
-    """Time the oracle's f16-faithful restatement of the reference's tiled kernel on a bounded
-    sample of each workload's layer, scale to 28 layers, return tokens/s over the same step."""
+    """The JS restatement under Node: parity-checked on config 0, then timed on one thread and on
+    N worker threads over bounded samples; per-layer times scaled by visited-tile counts and to
+    28 layers; tokens/s over the same step as the GPU value."""
+    node = shutil.which("node")
+    if node is None:
+        raise RuntimeError("node is not installed on this host")
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle
-    threads = oracle.get_threads()
-    total_s = 0.0
-    samples = []
-    for name in selected:
-        cfg, lengths, mask, _ = WORKLOADS[name]
-        if len(lengths) > 1:
-            # whole sequences: 4 of the batch (all equal length), scaled by nseq / 4
-            k = min(4, len(lengths))
-            sub = lengths[:k]
-            cu = np.concatenate([[0], np.cumsum(sub)]).astype(np.int32)
-            qh, kh, vh = oracle.gen_qkv(cfg, 0, cu)
-            t0 = time.perf_counter()
-            oracle.attention_tiled16(qh, kh, vh, cu, kind=mask)
-            dt = time.perf_counter() - t0
-            layer_s = dt * len(lengths) / k
-            samples.append(f"{name}: {k} of {len(lengths)} sequences of layer 0")
-        else:
-            # every 4th 16-query tile of the single sequence, scaled by the tile count ratio
+    js = os.path.join(REPO, "oracle", "tiled16.js")
+    nthreads = min(CPU_THREADS_MAX, len(os.sched_getaffinity(0)))
+    version = subprocess.run([node, "--version"], capture_output=True, text=True).stdout.strip()
+    with tempfile.TemporaryDirectory() as tmp:
+        def stage(cfg, cu, kind, sample=None):
+            q, k, v = oracle.gen_qkv(cfg, 0, cu)
+            q.tofile(os.path.join(tmp, "q.bin"))
+            k.tofile(os.path.join(tmp, "k.bin"))
+            v.tofile(os.path.join(tmp, "v.bin"))
+            meta = {"cu": [int(x) for x in cu], "kind": kind, "prefix": 176, "window": 432}
+            if sample is not None:
+                meta["sample"] = sample
+            with open(os.path.join(tmp, "meta.json"), "w") as f:
+                json.dump(meta, f)
+            return q, k, v
+
+        # parity first: config 0 through the JS restatement equals the C restatement bit for bit
+        cu0 = np.array([0, 50], np.int32)
+        q, k, v = stage(0, cu0, 1)
+        subprocess.run([node, js, "run", tmp], check=True, timeout=120)
+        got = np.fromfile(os.path.join(tmp, "o.bin"), np.uint16).reshape(50, 2048)
+        want = oracle.attention_tiled16(q, k, v, cu0, kind=1).reshape(50, 2048)
+        if not np.array_equal(got, want):
+            raise RuntimeError(f"JS restatement differs from the C one on config 0 "
+                               f"({int((got != want).sum())} values)")
+        log(f"cpu baseline: node {version}: JS restatement equals the C one on config 0 (bit for bit)")
+
+        layer_s = {1: 0.0, nthreads: 0.0}
+        notes = []
+        for name in selected:
+            lengths = lengths_of(name)
+            cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+            if len(lengths) > 1:
+                cu = cu[:2]  # sequence 0 carries the sample (the sequences are alike)
+            for threads in (1, nthreads):
+                sample, scale, kind = node_samples(name, threads)
+                stage(WORKLOADS[name][0], cu, kind, sample)
+                r = subprocess.run([node, js, "time", tmp, str(threads)], capture_output=True,
+                                   text=True, timeout=600, check=True)
+                rep = json.loads(r.stdout.strip().splitlines()[-1])
+                layer_s[threads] += rep["seconds"] * scale
+                log(f"cpu baseline {name}: {len(sample)} groups on {threads} thread(s): "
+                    f"{rep['seconds']:.2f} s -> {rep['seconds'] * scale:.1f} s per layer")
+            notes.append(f"{name}: 1 in {2 if name == 'full' else 16} 16-query tiles of sequence 0 "
+                         f"x 1 head per thread (scaled by visited 16-key tiles)")
+        # The C port (OpenMP) as a cross-check of the JS figures.
+        c_threads = oracle.get_threads()
+        c_layer_s = 0.0
+        for name in selected:
+            lengths = lengths_of(name)
             L = lengths[0]
-            cu = np.array([0, L], dtype=np.int32)
-            qh, kh, vh = oracle.gen_qkv(cfg, 0, cu)
-            ntiles = (L + 15) // 16
+            cu = np.array([0, L], np.int32)
+            q, k, v = oracle.gen_qkv(WORKLOADS[name][0], 0, cu)
+            vt = visited_key_tiles(L, WORKLOADS[name][2])
             step = 4
-            done = len(range(0, ntiles, step))
             t0 = time.perf_counter()
-            oracle.attention_tiled16_tiles(qh, kh, vh, cu, 0, 0, ntiles, step, kind=mask)
+            oracle.attention_tiled16_tiles(q, k, v, cu, 0, 0, len(vt), step, kind=WORKLOADS[name][2])
             dt = time.perf_counter() - t0
-            layer_s = dt * ntiles / done
-            samples.append(f"{name}: every {step}th 16-query tile ({done} of {ntiles}) of layer 0")
-        log(f"cpu baseline {name}: sample {dt:.2f} s -> {layer_s:.2f} s per layer")
-        total_s += layer_s * LAYERS
-    tokens = sum(sum(WORKLOADS[n][1]) for n in selected) * LAYERS
+            c_layer_s += dt * sum(vt) * len(lengths) / sum(vt[::step])
+    tokens = sum(sum(lengths_of(n)) for n in selected) * LAYERS
     return {
-        "value": tokens / total_s,
+        "value": tokens / (layer_s[nthreads] * LAYERS),
         "unit": "tokens/s",
-        "cores": threads,
+        "cores": nthreads,
         "kind": "port",
-        "sample": "; ".join(samples) + f"; x{LAYERS} layers; f16-faithful restatement of the "
-                  "reference's 16x16 tiled WGSL kernel (oracle/oracle.c, OpenMP)",
+        "sample": "; ".join(notes) + f"; x{LAYERS} layers; the reference's 16x16 tiled WGSL kernel "
+                  "(ops.ts:168-241) restated in JavaScript (oracle/tiled16.js, f16 rounding points "
+                  "as the WGSL), bit-identical to the C restatement on config 0",
+        "runtime": f"node {version}, worker_threads",
+        "single_thread_value": tokens / (layer_s[1] * LAYERS),
+        "host_cpus": os.cpu_count(),
+        "c_port_cross_check": {"value": tokens / (c_layer_s * LAYERS), "cores": c_threads,
+                               "kind": "port", "runtime": "oracle/oracle.c, OpenMP"},
     }
 
+
+# ---- auxiliary timings --------------------------------------------------------------------------
 
 def copy_calibration(mib):
     """Five copies of `mib` MiB between two device buffers: each dispatch reads and writes exactly
@@ -223,6 +339,16 @@ def q4_timing(reps):
     ctx.close()
 
 
+def kernel_sources_sha():
+    """Hash of the sources the attention launch is built from: HBM traffic measured on other
+    sources (profiles/traffic.json) is not reported as this build's."""
+    h = hashlib.sha256()
+    for f in ("attn_fwd.hip", "attn_common.h", "api.hip"):
+        with open(os.path.join(PKG, "csrc", f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -230,6 +356,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", choices=sorted(SETS), default="both")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the other BASELINE configs in the breakdown")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device copies of MIB MiB (torch copy_) and exit: the "
                          "known-size reference for rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -258,10 +386,12 @@ def main():
     log(f"device {dev} ({cus} CUs)")
     selected = SETS[args.workload]
     wls = [Workload(ctx, q, n) for n in selected]
-    for w in wls:
+    extra = [] if (args.no_extra or args.workload != "both") else [Workload(ctx, q, n) for n in EXTRA]
+    for w in wls + extra:
         i = w.info
         log(f"{w.name}: {w.desc_text}: tokens {i.tokens}, pairs {i.pairs}, work items {i.work_items}, "
-            f"flops/launch {i.flops:.4e}, bytes/launch {i.bytes:.4e}, tile waste {i.tile_pairs / i.pairs:.3f}")
+            f"flops/launch {i.flops:.4e}, bytes/launch {i.bytes:.4e}, tile waste {i.tile_pairs / i.pairs:.3f}, "
+            f"split items {i.split_items}")
 
     def step():
         for w in wls:
@@ -285,12 +415,15 @@ def main():
     ms_per_step = region_ms / args.steps
     log(f"timed {args.steps} steps: {region_ms:.3f} ms on device events ({host_ms:.3f} ms host)")
 
-    # ---- per-launch kernel durations (separate pass, same launches) ----
+    # ---- per-launch kernel durations (separate pass, same launches; the other configs too) ----
     reps = max(3, min(args.steps, 10))
-    per = {w.name: [] for w in wls}
+    per = {w.name: [] for w in wls + extra}
     evs = [(ctx.event(), ctx.event()) for _ in range(LAYERS)]
+    for w in extra:
+        for _ in range(3):
+            w.encode_all()
     for _ in range(reps):
-        for w in wls:
+        for w in wls + extra:
             for r, (a, b) in zip(w.runs, evs):
                 a.record()
                 r.encode()
@@ -307,10 +440,11 @@ def main():
     total_bytes = sum(w.info.bytes for w in wls) * LAYERS
     kern_ms_step = sum(np.mean(per[w.name]) * LAYERS for w in wls)
     breakdown = {}
-    for w in wls:
+    for w in wls + extra:
         avg = float(np.mean(per[w.name]))
         breakdown[w.name] = {
             "workload": w.desc_text,
+            "headline": w in wls,
             "kernel_avg_us": round(avg * 1e3, 3),
             "tokens_per_s": round(w.tokens / (avg / 1e3), 1),
             "tflops": round(w.info.flops / (avg / 1e3) / 1e12, 2),
@@ -321,13 +455,23 @@ def main():
         log(f"{w.name}: kernel avg {avg * 1e3:.2f} us, {breakdown[w.name]}")
     achieved = total_flops / (kern_ms_step / 1e3) / 1e12
 
-    traffic = None
+    traffic, traffic_note = None, "no profiles/traffic.json"
     tpath = os.path.join(REPO, "profiles", "traffic.json")
     if os.path.exists(tpath):
         try:
-            traffic = json.load(open(tpath)).get(args.workload)
+            tj = json.load(open(tpath))
+            if tj.get("sources_sha") == kernel_sources_sha():
+                traffic = tj.get(args.workload)
+                traffic_note = ("HBM bytes per launch (mean over the step's launches), rocprofv3 "
+                                "FETCH_SIZE x2.0 + WRITE_SIZE x1.0 (copy-calibrated), profiles/traffic.json, "
+                                "measured on these kernel sources")
+            else:
+                traffic_note = ("profiles/traffic.json was measured on other kernel sources "
+                                f"({tj.get('sources_sha')} vs {kernel_sources_sha()}): not reported")
         except (ValueError, OSError):
             traffic = None
+    for w in extra:
+        w.free()
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -364,8 +508,7 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
             "traffic": traffic,
-            "traffic_note": "HBM bytes per launch (mean over the step's launches), rocprofv3 "
-                            "FETCH_SIZE x2.0 + WRITE_SIZE x1.0 (copy-calibrated), profiles/traffic.json",
+            "traffic_note": traffic_note,
             "kernel": "attn_fwd_kernel (+ attn_merge_kernel on split-K plans)",
             "algorithmic_flops_per_step": total_flops,
             "algorithmic_bytes_per_step": total_bytes,

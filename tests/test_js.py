@@ -54,3 +54,42 @@ def test_node_packer_equals_oracle_packer(oracle, tmp_path):
     got = np.frombuffer((tmp_path / "out.bin").read_bytes(), np.uint8)
     want, _, n = oracle.pack_q40_tile32([(k, 70, a.tobytes()), (k, 33, b.tobytes())])
     assert n == 103 and np.array_equal(got, want)
+
+
+@pytest.mark.skipif(shutil.which("node") is None, reason="node is not installed")
+@pytest.mark.parametrize("config,lengths,kind,groups", [
+    (0, [50], 1, None), (1, [40, 33, 1], 0, None),
+    # the sparse skip: the last query tiles of a 700-token sequence (rows 640..699), two heads
+    (3, [700], 1, [[0, t, h] for t in (40, 41, 42, 43) for h in (0, 13)])])
+def test_node_cpu_baseline_equals_c_restatement(oracle, tmp_path, config, lengths, kind, groups):
+    # oracle/tiled16.js (the Node CPU baseline bench.py times) against orc_attention_tiled16 (the C
+    # restatement of the same WGSL): bit for bit on every computed row.
+    import json
+    import numpy as np
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    q, k, v = oracle.gen_qkv(config, 0, cu)
+    for name, a in (("q", q), ("k", k), ("v", v)):
+        a.tofile(str(tmp_path / f"{name}.bin"))
+    meta = {"cu": cu.tolist(), "kind": kind, "prefix": 176, "window": 432}
+    if groups:
+        meta["sample"] = groups
+    (tmp_path / "meta.json").write_text(json.dumps(meta))
+    js = os.path.join(HERE, "..", "oracle", "tiled16.js")
+    r = subprocess.run(["node", js, "run", str(tmp_path)], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr
+    got = np.fromfile(str(tmp_path / "o.bin"), np.uint16).reshape(-1, 16, 128)
+    want = oracle.attention_tiled16(q, k, v, cu, kind=kind).reshape(got.shape)
+    if not groups:
+        assert np.array_equal(got, want)
+        return
+    for s, t, h in groups:
+        rows = slice(int(cu[s]) + 16 * t, min(int(cu[s]) + 16 * t + 16, int(cu[s + 1])))
+        assert np.array_equal(got[rows, h], want[rows, h]), (t, h)
+
+
+def test_bench_config1_lengths_equal_the_oracle_generator(oracle):
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("bench", os.path.join(HERE, "..", "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    assert bench.config1_lengths() == oracle.gen_lengths(oracle.seed(1, 0, 3), 16).tolist()
