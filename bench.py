@@ -300,6 +300,40 @@ def pool_timing(reps):
     ctx.close()
 
 
+def rope_timing(reps):
+    """The producer alone (not the headline metric): qattn_qk_norm_rope_qkv over one layer of the
+    16 x 500 packing -- qkvRaw [8000, 4096] -> compact Q [8000, 2048] and K [8000, 1024], RMSNorm
+    with gains + RoPE -- `reps` back-to-back launches between HIP events on the context stream.
+    Algorithmic bytes = 8000 tokens x 3072 values x (2 read + 2 written)."""
+    q = load_binding()
+    ctx = q.Context(0)
+    cu = np.concatenate([[0], np.cumsum([500] * 16)]).astype(np.int32)
+    T = int(cu[-1])
+    x, bq, bk = ctx.alloc(T * 4096 * 2), ctx.alloc(T * 2048 * 2), ctx.alloc(T * 1024 * 2)
+    w = ctx.upload(np.ones(256, np.float32))
+    ctx.fill_normal(x.ptr, T, 4096, 4096, 5)
+    for _ in range(10):
+        ctx.qk_norm_rope_qkv(x.ptr, bq.ptr, bk.ptr, cu, q_weight_ptr=w.ptr, k_weight_ptr=w.ptr + 512)
+    e0, e1 = ctx.event(), ctx.event()
+    ctx.synchronize()
+    e0.record()
+    for _ in range(reps):
+        ctx.qk_norm_rope_qkv(x.ptr, bq.ptr, bk.ptr, cu, q_weight_ptr=w.ptr, k_weight_ptr=w.ptr + 512)
+    e1.record()
+    ctx.synchronize()
+    us = e0.elapsed_ms(e1) * 1000.0 / reps
+    nbytes = T * 3072 * 4
+    print(json.dumps({"kernel": "qk_norm_rope_kernel", "workload": "16x500 qkvRaw -> Q, K", "tokens": T,
+                      "launches": reps, "us_per_launch": round(us, 3), "bytes": nbytes,
+                      "GB/s": round(nbytes / us / 1e3, 1),
+                      "hbm_frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 3)}), flush=True)
+    for b in (x, bq, bk, w):
+        b.free()
+    e0.destroy()
+    e1.destroy()
+    ctx.close()
+
+
 def q4_timing(reps):
     """The projection kernel alone (not the headline metric): qattn_q4_matmul at the shapes one
     layer of the 16 x 500 packing multiplies (M = 8000 tokens): the fused QKV projection
@@ -340,10 +374,10 @@ def q4_timing(reps):
 
 
 def kernel_sources_sha():
-    """Hash of the sources the attention launch is built from: HBM traffic measured on other
-    sources (profiles/traffic.json) is not reported as this build's."""
+    """Hash of the sources the attention launch is built from (kernels and planner): HBM traffic
+    measured on other sources (profiles/traffic.json) is not reported as this build's."""
     h = hashlib.sha256()
-    for f in ("attn_fwd.hip", "attn_common.h", "api.hip"):
+    for f in ("attn_fwd.hip", "attn_common.h", "planner.h", "planner.cpp"):
         with open(os.path.join(PKG, "csrc", f), "rb") as fh:
             h.update(fh.read())
     return h.hexdigest()[:16]
@@ -365,7 +399,12 @@ def main():
                     help="only time N launches of the last-token pool kernel per width and exit")
     ap.add_argument("--q4", type=int, default=0, metavar="N",
                     help="only time N launches of the Q4_0 dequant-GEMM per projection shape and exit")
+    ap.add_argument("--rope", type=int, default=0, metavar="N",
+                    help="only time N launches of the fused QK-norm + RoPE producer and exit")
     args = ap.parse_args()
+    if args.rope:
+        rope_timing(args.rope)
+        return
     if args.q4:
         q4_timing(args.q4)
         return

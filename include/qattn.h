@@ -13,8 +13,8 @@
  *   plan.destroy() of run.ownedBuffers model.ts:108-111 | qattn_run_destroy
  *   tiled flash attention shader       ops.ts:168-241   | kernel behind qattn_run_encode
  *   mask predicate + tile skip         ops.ts:205-220   | qattn_debug_run_mask (executed), _debug_mask
- *   QKNormRopeKernel                   ops.ts:104-166   | qattn_qk_norm_rope
- *   RoPE table                         model.ts:76-83   | built inside qattn_qk_norm_rope
+ *   QKNormRopeKernel                   ops.ts:104-166   | qattn_qk_norm_rope_qkv (_rope in place)
+ *   RoPE table                         model.ts:76-83   | cached per context by the producer
  *   last-token row of poolShader       ops.ts:357       | qattn_run_desc.o_last
  *   LastTokenPoolKernel (L2 norm)      ops.ts:347-379   | qattn_pool_last_l2
  *   compact Q4_0 batch matmul   quant-matmul.ts:267-307 | qattn_q4_matmul
@@ -207,9 +207,22 @@ int qattn_debug_run_mask(qattn_run* run, uint32_t* host_bits, int64_t capacity_w
                          int32_t* words_per_row);
 
 /* ---- producer: QK RMSNorm + RoPE  (replaces QKNormRopeKernel, ops.ts:104-166) ------------- */
-/* In place on fp16 rows: for each token and each of `heads` 128-wide vectors at element
- * t*row_stride + col0 + h*128: RMSNorm (eps, gain `weight` f32[128] device or NULL for 1), then
- * NeoX rotate-half RoPE with theta at the token's position inside its sequence. */
+/* Reads the Q block (16 heads, columns 0..2047) and K block (8 heads, 2048..3071) of each qkvRaw
+ * row (model.ts:69; row t at qkv + t*qkv_row_stride) and writes compact Q [T,16,128] and K
+ * [T,8,128] (row strides q_row_stride >= 2048, k_row_stride >= 1024): per 128-wide head vector,
+ * RMSNorm with eps and gain (q_weight / k_weight: f32[128] device arrays, NULL for 1), then NeoX
+ * rotate-half RoPE with theta at the token's position inside its sequence -- the reference's
+ * createRun(input, qWeight, kWeight, qOutput, kOutput, tokens, sequence, epsilon, ropeTable,
+ * inputStride) (ops.ts:157-165), in f32 as its shader.  The RoPE table (model.ts:76-83) is
+ * built once per context and rebuilt only when a longer sequence or another theta arrives;
+ * otherwise the call only enqueues (one launch per 64 sequences).  Pointers 16-byte aligned,
+ * strides multiples of 8 elements. */
+int qattn_qk_norm_rope_qkv(qattn_ctx* ctx, const void* qkv, int64_t qkv_row_stride, void* q,
+                           int64_t q_row_stride, void* k, int64_t k_row_stride,
+                           const int32_t* cu_seqlens, int32_t nseq, const float* q_weight,
+                           const float* k_weight, double eps, double theta, qattn_stream_t stream);
+/* The same math in place on one block of `heads` head vectors (a multiple of 4) per row, at
+ * element t*row_stride + col0 + h*128 (col0, row_stride multiples of 8), one gain for all. */
 int qattn_qk_norm_rope(qattn_ctx* ctx, void* x, int64_t row_stride, int64_t col0, int32_t heads,
                        const int32_t* cu_seqlens, int32_t nseq, const float* weight, double eps,
                        double theta, qattn_stream_t stream);

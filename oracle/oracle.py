@@ -19,7 +19,8 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "liboracle.so")
+# QATTN_ORACLE_LIB selects another build (the sanitizer build of tests/sanitize.sh).
+LIB_PATH = os.environ.get("QATTN_ORACLE_LIB") or os.path.join(HERE, "liboracle.so")
 
 MASK_CAUSAL = 0
 MASK_PREFIX_LOCAL = 1

@@ -1,13 +1,8 @@
 // api.hip -- the C ABI declared in include/qattn.h: context, buffers, the attention operator
 // (planner + launch), the mask check, the QK-norm/RoPE producer and the input generator.
 //
-// Planner (replaces CausalAttentionKernel.createRun, src/webgpu/ops.ts:327-343): the reference
-// bakes [batch, sequence, heads, value_stride, value_offset] into a uniform buffer and
-// dispatches ceil(S/16) x batch*16 workgroups over a padded batch.  Here a run holds a device
-// work list of (sequence, KV head, 64-query block) items built from cu_seqlens: no padded rows,
-// both heads of a GQA group per item, heaviest items first so the longest causal rows start
-// early, and one launch per layer regardless of sequence length (the reference switches to a
-// chunked two-pass path above 8192 tokens, ops.ts:328-342; this kernel has no such limit).
+// A run (CausalAttentionKernel.createRun, src/webgpu/ops.ts:327-343) validates its description,
+// plans it (planner.cpp) and holds the work list in device memory for every later encode.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -22,6 +17,8 @@
 
 #include "../../include/qattn.h"
 #include "attn_common.h"
+#include "planner.h"
+#include "qk_rope.h"
 
 namespace qattn {
 hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream);
@@ -37,10 +34,6 @@ hipError_t launch_q4_matmul(const half_t* x, int64_t ldx, int M, int K, const ui
                             half_t* y, int64_t ldy, hipStream_t stream);
 hipError_t launch_pool_last_l2(const half_t* x, int64_t row_stride, int width, const int32_t* cu_seqlens,
                                int nseq, float* out, int64_t out_row_stride, hipStream_t stream);
-hipError_t launch_qk_norm_rope(half_t* x, int64_t row_stride, int64_t col0, int heads,
-                               const int32_t* cu_dev, int nseq, int64_t T, const float* weight,
-                               double eps, const float* rope_cos, const float* rope_sin,
-                               hipStream_t stream);
 }  // namespace qattn
 
 using namespace qattn;
@@ -61,6 +54,11 @@ struct qattn_ctx {
   int cu_count = 0;
   hipStream_t stream = nullptr;
   void* scratch = nullptr;  // this device's copy of `scratch` (qattn_prefill_static)
+  // RoPE table of the producer, [positions][64] (cos, sin), built for `rope_theta`; grown when a
+  // longer sequence arrives (the reference builds one per plan, model.ts:76-83).
+  float2* rope = nullptr;
+  int32_t rope_positions = 0;
+  double rope_theta = 0.0;
   std::string last_error;
   std::mutex mu;
 };
@@ -173,21 +171,6 @@ int validate_desc(qattn_ctx* ctx, const qattn_run_desc* d) {
   return QATTN_OK;
 }
 
-int64_t pairs_of(int64_t L, const MaskSpec& m) {
-  // Closed form of the retained-pair count (sum over q of |{k : retained(q,k)}|).
-  if (L <= 0) return 0;
-  if (m.kind == 0) return L * (L + 1) / 2;
-  int64_t total = 0;
-  const int64_t ps = std::min<int64_t>(L, m.prefix), ws = std::min<int64_t>(L, m.window);
-  for (int64_t q = 0; q < L; ++q) {
-    // keys [0, min(q, ps-1)] U [max(0, q-ws+1), q]
-    const int64_t a = std::min<int64_t>(q + 1, ps);    // prefix part
-    const int64_t wlo = std::max<int64_t>(0, q - ws + 1);
-    const int64_t b = q + 1 - std::max<int64_t>(wlo, a);  // window part not already counted
-    total += a + std::max<int64_t>(0, b);
-  }
-  return total;
-}
 
 }  // namespace
 
@@ -241,6 +224,7 @@ void qattn_destroy(qattn_ctx* ctx) {
       (void)hipStreamSynchronize(ctx->stream);
       (void)hipStreamDestroy(ctx->stream);
     }
+    if (ctx->rope) (void)hipFree(ctx->rope);
   }
   delete ctx;
 }
@@ -317,359 +301,6 @@ int qattn_buffer_fill_u16(qattn_ctx* ctx, void* dst, uint16_t value, size_t coun
 
 }  // extern "C"
 
-namespace {
-
-// Slots: persistent workgroups of one launch.  Two fit on a CU (64 KiB LDS, <= 256 VGPRs each);
-// workgroup b is dispatched to XCD b % kXcds, so the planner puts every item of KV head g on
-// slots b = kXcds * j + g % kXcds and that head's K/V tiles stay in one XCD's L2.
-constexpr int kXcds = 8;
-constexpr int kBlocksPerCU = 2;
-constexpr int kDefaultSlots = 256 * kBlocksPerCU;  // MI355X: 256 CUs
-// Partial result of one chunk: per wavefront (4) and lane (64), the 64 fp32 O^T accumulators
-// of the lane's row, then m and l (log2-domain row max, row sum) and two pad words.
-constexpr int kPartialFloats = 68;
-constexpr size_t kPartialBytes = (size_t)kWaves * 64 * kPartialFloats * 4;
-
-struct Plan {
-  std::vector<WorkItem> items;       // grouped by slot, heaviest first within a slot
-  std::vector<int32_t> slot_begin;   // n_slots + 1 offsets into items
-  std::vector<WorkItem> split_heads; // chunk 0 of each split item, by split id
-  int32_t splits = 0;                // items spread over several chunks
-  int32_t partials = 0;              // chunk partial-result records the workspace holds
-};
-
-// Cost model for load balancing, in quarter tiles (one 64-key tile of an entry = 4), fitted to
-// the measured duration of every workgroup of the 16x500 and 1x5000 benchmark launches (start
-// and end s_memtime of each workgroup of an instrumented build, 28 HBM-resident layers; least
-// squares over 1024 workgroups, residual 2.6%):
-//   duration = speed x (tiles + 3.3 entries + 4.6) tile times,
-// speed 1 for the first workgroup of a CU and 1.3 for the second (the CUs issue from their
-// oldest wavefronts first).  An entry's start and end (Q and first K tiles, last PV, O stores)
-// cost about three tiles that the pipeline does not hide, a workgroup's start (all launch
-// together, so their first loads queue at HBM) and end about four and a half, and a chunk of a
-// split item no more than any other entry.  Refits on other plans gave 2.2-3.3 tiles per entry
-// and 1.2-1.3 for the second workgroup; these constants measured fastest among them (16x500:
-// 37.5 us with the previous 0.75-tile entries and 1.2 factor, 35.6 us with these).
-constexpr int kEntryCost = 13;
-int item_cost(int ntiles) { return 4 * ntiles + kEntryCost; }
-constexpr int kSlotBase = 18;
-constexpr int kChunkExtra = 0;
-constexpr int kMinChunkTiles = 2;
-// Slot speeds, in time per unit of cost (per mille): slots cu_count..2*cu_count-1 (an XCD's
-// first 32 workgroups take one CU each) are the second workgroups.
-constexpr int64_t kFirstSlotTime = 1000;
-constexpr int64_t kSecondSlotTime = 1300;
-
-// The planner: validated description -> work entries grouped into slots + run figures.
-int plan_work(qattn_ctx* ctx, const qattn_run_desc* d, int max_slots, Plan* out,
-              qattn_run_info* info_out, MaskSpec* mask_out) {
-  int rc = validate_desc(ctx, d);
-  if (rc) return rc;
-  if (max_slots < kXcds) max_slots = kXcds;
-  const MaskSpec mask{d->mask, d->mask == QATTN_MASK_PREFIX_LOCAL ? d->prefix : 0,
-                      d->mask == QATTN_MASK_PREFIX_LOCAL ? d->window : 0};
-  struct Item {
-    WorkItem w;
-    int ntiles;
-    int order;  // position in sequence-major order (sequence, then query block)
-  };
-  std::vector<Item> group_items[kXcds];
-  qattn_run_info info{};
-  info.block_queries = kBlockQ;
-  for (int32_t s = 0; s < d->nseq; ++s) {
-    const int start = d->cu_seqlens[s];
-    const int L = d->cu_seqlens[s + 1] - start;
-    info.tokens += L;
-    info.pairs += pairs_of(L, mask);
-    for (int qb = 0; qb * kBlockQ < L; ++qb) {
-      const int q0 = qb * kBlockQ, q1 = std::min(L, q0 + kBlockQ) - 1;
-      const TileRanges tr = key_tiles(q0, q1, L, mask);
-      // MFMA tile work of one query head: the wavefronts holding rows [q0, q0+31] and
-      // [q0+32, q0+63] each compute every tile of the work item.
-      info.tile_pairs += (int64_t)tr.count() * (q0 + kWaveQ < L ? 2 : 1) * kWaveQ * kTileK;
-      for (int g = 0; g < kKVHeads; ++g)
-        group_items[g % kXcds].push_back({WorkItem{start, L, qb, (s << 4) | g, 0, tr.count(), -1, 0}, tr.count(),
-                                          (int)group_items[g % kXcds].size()});
-      ++info.work_items;
-    }
-  }
-  info.work_items *= kKVHeads;
-  // Per XCD group, longest processing time first with split-K: items in falling cost (stable,
-  // so equal items keep sequence order) each go whole to the least loaded slot if that keeps it
-  // within a target makespan T; otherwise the item is cut into chunks of key tiles that fill the
-  // least loaded slots up to T (the chunks' partial softmax states are merged by a second
-  // kernel).  T is scanned upward from the mean load; the plan with the smallest
-  // makespan (then fewest chunks) wins.
-  const int per_group = max_slots / kXcds;
-  const bool may_split = !(d->flags & QATTN_FLAG_BATCH_INVARIANT);
-  std::vector<std::vector<WorkItem>> lists[kXcds];
-  int used = 0;
-  for (int g = 0; g < kXcds; ++g) {
-    auto& items = group_items[g];
-    std::stable_sort(items.begin(), items.end(), [](const Item& a, const Item& b) { return a.ntiles > b.ntiles; });
-    const int m = std::min<int>(per_group, (int)items.size());
-    if (!m) continue;
-    int64_t total = 0;  // the group's cost, workgroup bases included
-    int max_tiles = 0;
-    for (const Item& it : items) {
-      total += item_cost(it.ntiles);
-      max_tiles = std::max(max_tiles, it.ntiles);
-    }
-    total += (int64_t)m * kSlotBase;
-    // Slot j of this group is global slot kXcds * j + g: the first half of the group's share
-    // of the launch are first workgroups on their CUs.  Loads are in cost units; finish times
-    // (load x time per unit) are what the plans balance.
-    const int first_slots = std::max(1, per_group / kBlocksPerCU);
-    std::vector<int64_t> slot_time(m);
-    for (int j = 0; j < m; ++j) slot_time[j] = j < first_slots ? kFirstSlotTime : kSecondSlotTime;
-    auto span_of = [&](const std::vector<int64_t>& load) {
-      int64_t span = 0;
-      for (int j = 0; j < m; ++j) span = std::max(span, load[j] * slot_time[j]);
-      return span;
-    };
-    // One greedy pass for target finish time T: per item, (slot, tile range) pieces; returns the
-    // makespan.
-    struct Piece {
-      int slot, item, a, b, cost;
-    };
-    auto greedy = [&](int64_t T, std::vector<Piece>* pieces, int* nchunks) {
-      std::vector<int64_t> load(m, kSlotBase);
-      // One min-heap of (load, slot) per speed class: within a class the least loaded slot
-      // both finishes first and has the most room under T.
-      typedef std::pair<int64_t, int> Entry;
-      std::vector<Entry> heap[2];
-      for (int j = 0; j < m; ++j) heap[j < first_slots ? 0 : 1].push_back({0, j});
-      auto cmp = [](const Entry& x, const Entry& y) { return x > y; };
-      for (auto& h : heap) std::make_heap(h.begin(), h.end(), cmp);
-      auto top = [&](int c) { return heap[c].empty() ? -1 : heap[c].front().second; };
-      auto take_out = [&](int j) {
-        auto& h = heap[j < first_slots ? 0 : 1];
-        std::pop_heap(h.begin(), h.end(), cmp);
-        h.pop_back();
-      };
-      auto put_back = [&](int j) {
-        auto& h = heap[j < first_slots ? 0 : 1];
-        h.push_back({load[j], j});
-        std::push_heap(h.begin(), h.end(), cmp);
-      };
-      // The class top that finishes first after adding cost c.
-      auto earliest = [&](int64_t c) {
-        const int a = top(0), b = top(1);
-        if (a < 0) return b;
-        if (b < 0) return a;
-        return (load[a] + c) * slot_time[a] <= (load[b] + c) * slot_time[b] ? a : b;
-      };
-      // Room under T (cost units) of slot j.
-      auto room = [&](int j) { return T / slot_time[j] - load[j]; };
-      pieces->clear();
-      *nchunks = 0;
-      for (int i = 0; i < (int)items.size(); ++i) {
-        const int n = items[i].ntiles;
-        int j = earliest(item_cost(n));
-        if ((load[j] + item_cost(n)) * slot_time[j] <= T || n < 2 * kMinChunkTiles || !may_split) {
-          take_out(j);
-          load[j] += item_cost(n);
-          pieces->push_back({j, i, 0, n, item_cost(n)});
-          put_back(j);
-          continue;
-        }
-        std::vector<Piece> mine;
-        int a = 0;
-        while (a < n) {
-          const int rest = n - a;
-          // The class top with the most room under T takes a chunk that fills it; if no
-          // slot has room for a chunk, the rest goes whole to the slot that finishes it first.
-          const int x = top(0), y = top(1);
-          j = x < 0 ? y : y < 0 ? x : (room(x) >= room(y) ? x : y);
-          int take = (int)((room(j) - kEntryCost - kChunkExtra) / 4);
-          if (take < kMinChunkTiles || (int)mine.size() == kMaxChunks - 1 || take >= rest ||
-              rest - take < kMinChunkTiles) {
-            take = rest;
-            j = earliest(item_cost(rest) + kChunkExtra);
-          }
-          take_out(j);
-          mine.push_back({j, i, a, a + take, item_cost(take) + kChunkExtra});
-          load[j] += item_cost(take) + kChunkExtra;
-          put_back(j);
-          a += take;
-        }
-        if (mine.size() == 1) {  // not split after all
-          load[mine[0].slot] -= kChunkExtra;
-          mine[0].cost -= kChunkExtra;
-        } else {
-          *nchunks += (int)mine.size();
-        }
-        pieces->insert(pieces->end(), mine.begin(), mine.end());
-      }
-      return span_of(load);
-    };
-    // Rounds plan (whole items, for L2 locality): items in sequence-major order, m per round,
-    // so the slots of an XCD work on the same few sequences at a time; within a round the
-    // heaviest items go to the slots that would finish first.
-    auto rounds = [&](std::vector<Piece>* pieces) {
-      std::vector<int> seq_order(items.size());
-      for (int i = 0; i < (int)items.size(); ++i) seq_order[items[i].order] = i;
-      std::vector<int64_t> load(m, kSlotBase);
-      std::vector<int> slot_ix(m);
-      pieces->clear();
-      for (size_t r0 = 0; r0 < seq_order.size(); r0 += m) {
-        std::vector<int> its(seq_order.begin() + r0, seq_order.begin() + std::min(seq_order.size(), r0 + m));
-        std::stable_sort(its.begin(), its.end(), [&](int a, int b) { return items[a].ntiles > items[b].ntiles; });
-        for (int j = 0; j < m; ++j) slot_ix[j] = j;
-        std::stable_sort(slot_ix.begin(), slot_ix.end(), [&](int a, int b) {
-          return (load[a] + 1) * slot_time[a] < (load[b] + 1) * slot_time[b];
-        });
-        for (size_t k = 0; k < its.size(); ++k) {
-          const int j = slot_ix[k];
-          pieces->push_back({j, its[k], 0, items[its[k]].ntiles, item_cost(items[its[k]].ntiles)});
-          load[j] += item_cost(items[its[k]].ntiles);
-        }
-      }
-      return span_of(load);
-    };
-    // Local search on a plan.  Slots are visited from the one that finishes last; a slot hands
-    // one of its pieces to a slot that finishes earlier, or trades it for a cheaper piece there,
-    // when both then finish before it did.  Each move lowers the sorted vector of finish times
-    // lexicographically, so the search ends; the first slots' moves lower the makespan, the
-    // others make room for later ones.  Pieces only change slots: their order (each slot's
-    // entry order and the chunk order of split items) stays.
-    auto improve = [&](std::vector<Piece>* pieces) {
-      std::vector<int64_t> load(m, kSlotBase);
-      std::vector<std::vector<int>> held(m);
-      for (int k = 0; k < (int)pieces->size(); ++k) {
-        load[(*pieces)[k].slot] += (*pieces)[k].cost;
-        held[(*pieces)[k].slot].push_back(k);
-      }
-      auto fin = [&](int j, int64_t l) { return l * slot_time[j]; };
-      std::vector<int> order(m);
-      for (int moves = 0; moves < 8 * (int)pieces->size(); ++moves) {
-        for (int j = 0; j < m; ++j) order[j] = j;
-        std::sort(order.begin(), order.end(), [&](int a, int b) { return fin(a, load[a]) > fin(b, load[b]); });
-        bool moved = false;
-        for (int oj = 0; oj < m && !moved; ++oj) {
-          const int j = order[oj];
-          const int64_t fj = fin(j, load[j]);
-          for (int ok = m - 1; ok > oj && !moved; --ok) {
-            const int k = order[ok];
-            if (fin(k, load[k]) >= fj) break;
-            for (int pi : held[j]) {
-              const int cp = (*pieces)[pi].cost;
-              int qsel = -1;
-              bool ok_move = std::max(fin(j, load[j] - cp), fin(k, load[k] + cp)) < fj;
-              if (!ok_move) {
-                for (int qi : held[k]) {
-                  const int cq = (*pieces)[qi].cost;
-                  if (cq < cp && std::max(fin(j, load[j] - cp + cq), fin(k, load[k] - cq + cp)) < fj) {
-                    qsel = qi;
-                    break;
-                  }
-                }
-                if (qsel < 0) continue;
-              }
-              auto relocate = [&](int idx, int from, int to) {
-                held[from].erase(std::find(held[from].begin(), held[from].end(), idx));
-                held[to].push_back(idx);
-                (*pieces)[idx].slot = to;
-                load[from] -= (*pieces)[idx].cost;
-                load[to] += (*pieces)[idx].cost;
-              };
-              relocate(pi, j, k);
-              if (qsel >= 0) relocate(qsel, k, j);
-              moved = true;
-              break;
-            }
-          }
-        }
-        if (!moved) break;
-      }
-      return span_of(load);
-    };
-    std::vector<Piece> best, trial;
-    int64_t best_span = rounds(&best);
-    best_span = improve(&best);
-    int best_chunks = 0;
-    // Lower bound of the makespan: the total cost spread over the slots in proportion to their
-    // speeds.  Targets step by a quarter tile (one cost unit) on a first slot.
-    double rate = 0.0;
-    for (int j = 0; j < m; ++j) rate += 1.0 / (double)slot_time[j];
-    const int64_t lo = (int64_t)std::ceil((double)total / rate);
-    // LPT (whole items), then makespan-targeted split-K plans; a plan must be strictly better
-    // than the rounds plan to replace it.
-    for (int64_t T = lo; T <= lo + (4 * max_tiles + 8) * kFirstSlotTime && best_span > lo; T += kFirstSlotTime) {
-      int nch = 0;
-      const int64_t span = greedy(may_split ? T : INT64_MAX / 4, &trial, &nch);
-      if (span < best_span || (span == best_span && nch < best_chunks)) {
-        best_span = span;
-        best_chunks = nch;
-        best.swap(trial);
-      }
-      if (!may_split) break;
-    }
-    best_span = improve(&best);
-    // Emit: per slot in assignment order; chunks of one item share a split id and partials.
-    lists[g].assign(m, {});
-    for (size_t k = 0; k < best.size();) {
-      size_t e = k + 1;
-      while (e < best.size() && best[e].item == best[k].item) ++e;
-      const WorkItem base = items[best[k].item].w;
-      const int nch = (int)(e - k);
-      const int split = nch > 1 ? out->splits++ : -1;
-      const int first = nch > 1 ? out->partials : 0;
-      if (nch > 1) out->partials += nch;
-      for (size_t c = k; c < e; ++c) {
-        WorkItem w = base;
-        w.tile_begin = best[c].a;
-        w.tile_end = best[c].b;
-        w.split = split;
-        w.part = nch > 1 ? (int)(c - k) | (nch << 4) | (first << 8) : 0;
-        if (nch > 1 && c == k) out->split_heads.push_back(w);
-        lists[g][best[c].slot].push_back(w);
-      }
-      k = e;
-    }
-    used = std::max(used, m);
-  }
-  out->items.clear();
-  out->slot_begin.assign(1, 0);
-  for (int j = 0; j < used; ++j)
-    for (int g = 0; g < kXcds; ++g) {
-      if (j < (int)lists[g].size())
-        for (const WorkItem& w : lists[g][j]) out->items.push_back(w);
-      out->slot_begin.push_back((int32_t)out->items.size());
-    }
-  info.slots = (int32_t)out->slot_begin.size() - 1;
-  info.split_items = out->splits;
-  info.flops = 4ll * kHeadDim * kQHeads * info.pairs;
-  info.bytes = 12288ll * info.tokens + (d->o_last ? 4096ll * d->nseq : 0);
-  if (info_out) *info_out = info;
-  if (mask_out) *mask_out = mask;
-  return QATTN_OK;
-}
-
-// Launch arguments of a validated description whose work list sits at `plan` (entries, then the
-// split items' chunk-0 entries, then the slot offsets).
-void fill_params(AttnParams* p, const qattn_run_desc* d, const MaskSpec& mask, int32_t slots, const void* plan,
-                 size_t items_bytes, size_t heads_bytes) {
-  p->q = static_cast<const half_t*>(d->q);
-  p->k = static_cast<const half_t*>(d->k);
-  p->v = static_cast<const half_t*>(d->v) + d->v_offset;
-  p->o = static_cast<half_t*>(d->o);
-  p->o_last = static_cast<half_t*>(d->o_last);
-  // Byte strides fit 32 bits: (L + 64) * stride * 2 < 2^31 is validated for every sequence.
-  p->q_stride_b = (uint32_t)(d->q_row_stride * 2);
-  p->k_stride_b = (uint32_t)(d->k_row_stride * 2);
-  p->v_stride_b = (uint32_t)(d->v_row_stride * 2);
-  p->o_stride_b = (uint32_t)(d->o_row_stride * 2);
-  p->work = static_cast<const WorkItem*>(plan);
-  p->splits = reinterpret_cast<const WorkItem*>(static_cast<const char*>(plan) + items_bytes);
-  p->slot_begin = reinterpret_cast<const int32_t*>(static_cast<const char*>(plan) + items_bytes + heads_bytes);
-  p->n_slots = slots;
-  p->mask = mask;
-  p->scale_log2 = (float)(1.4426950408889634 / std::sqrt(128.0));
-}
-
-}  // namespace
-
 extern "C" {
 
 int qattn_plan_describe(const qattn_run_desc* desc, int32_t* items, int32_t capacity,
@@ -677,8 +308,9 @@ int qattn_plan_describe(const qattn_run_desc* desc, int32_t* items, int32_t capa
   if (!count) return fail(nullptr, QATTN_EINVAL, "count is NULL");
   Plan plan;
   qattn_run_info inf{};
-  int rc = plan_work(nullptr, desc, kDefaultSlots, &plan, &inf, nullptr);
+  int rc = validate_desc(nullptr, desc);
   if (rc) return rc;
+  plan_work(desc, kDefaultSlots, &plan, &inf, nullptr);
   *count = (int32_t)plan.items.size();
   if (info) *info = inf;
   if (items) {
@@ -694,8 +326,9 @@ int qattn_plan_slots(const qattn_run_desc* desc, int32_t max_slots, int32_t* slo
                      int32_t capacity, int32_t* nslots) {
   if (!nslots) return fail(nullptr, QATTN_EINVAL, "nslots is NULL");
   Plan plan;
-  int rc = plan_work(nullptr, desc, max_slots > 0 ? max_slots : kDefaultSlots, &plan, nullptr, nullptr);
+  int rc = validate_desc(nullptr, desc);
   if (rc) return rc;
+  plan_work(desc, max_slots > 0 ? max_slots : kDefaultSlots, &plan, nullptr, nullptr);
   *nslots = (int32_t)plan.slot_begin.size() - 1;
   if (slot_begin) {
     if (capacity < (int32_t)plan.slot_begin.size())
@@ -711,8 +344,9 @@ int qattn_run_create(qattn_ctx* ctx, const qattn_run_desc* d, qattn_run** out) {
   Plan plan;
   qattn_run_info info{};
   MaskSpec mask{};
-  int rc = plan_work(ctx, d, std::max(1, ctx->cu_count) * kBlocksPerCU, &plan, &info, &mask);
+  int rc = validate_desc(ctx, d);
   if (rc) return rc;
+  plan_work(d, std::max(1, ctx->cu_count) * kBlocksPerCU, &plan, &info, &mask);
 
   auto* run = new (std::nothrow) qattn_run();
   if (!run) return fail(ctx, QATTN_ENOMEM, "out of host memory");
@@ -830,8 +464,9 @@ int qattn_prefill_static(qattn_ctx* ctx, const qattn_run_desc* desc, qattn_strea
   Plan plan;
   qattn_run_info info{};
   MaskSpec mask{};
-  int rc = plan_work(ctx, &d, std::max(1, ctx->cu_count) * kBlocksPerCU, &plan, &info, &mask);
+  int rc = validate_desc(ctx, &d);
   if (rc) return rc;
+  plan_work(&d, std::max(1, ctx->cu_count) * kBlocksPerCU, &plan, &info, &mask);
   const size_t items_bytes = plan.items.size() * sizeof(WorkItem);
   const size_t slots_bytes = plan.slot_begin.size() * sizeof(int32_t);
   if (items_bytes + slots_bytes > kScratchBytes)
@@ -939,43 +574,120 @@ int qattn_plan_mask(int32_t L, int32_t mask, int32_t prefix, int32_t window, uin
 
 // ---- producer + generator ---------------------------------------------------------------------
 
+namespace {
+// The context's RoPE table covering `positions` positions for `theta` (model.ts:76-81: angle =
+// pos * theta^(-i/64) in f64, cos / sin rounded to f32), rebuilt only when it must grow or theta
+// changes.  A rebuild uploads synchronously; every other call only reads it.
+int rope_table(qattn_ctx* ctx, int32_t positions, double theta, const float2** out) {
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  if (ctx->rope && ctx->rope_positions >= positions && ctx->rope_theta == theta) {
+    *out = ctx->rope;
+    return QATTN_OK;
+  }
+  const int32_t n = std::max(positions, std::max(ctx->rope_positions, 1024));
+  std::vector<float2> table((size_t)n * 64);
+  for (int32_t pos = 0; pos < n; ++pos)
+    for (int i = 0; i < 64; ++i) {
+      const double angle = (double)pos * std::pow(theta, -(double)i / 64.0);
+      table[(size_t)pos * 64 + i] = float2{(float)std::cos(angle), (float)std::sin(angle)};
+    }
+  DeviceGuard g(ctx->device);
+  float2* dev = nullptr;
+  hipError_t e = hipMalloc(&dev, table.size() * sizeof(float2));
+  if (e != hipSuccess) {
+    ctx->last_error = std::string("RoPE table: ") + hipGetErrorString(e);
+    g_last_error = ctx->last_error;
+    return QATTN_ENOMEM;
+  }
+  e = hipMemcpy(dev, table.data(), table.size() * sizeof(float2), hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(dev);
+    ctx->last_error = std::string("RoPE table upload: ") + hipGetErrorString(e);
+    g_last_error = ctx->last_error;
+    return QATTN_EHIP;
+  }
+  if (ctx->rope) (void)hipFree(ctx->rope);  // waits for the device to be idle first
+  ctx->rope = dev;
+  ctx->rope_positions = n;
+  ctx->rope_theta = theta;
+  *out = dev;
+  return QATTN_OK;
+}
+
+int32_t longest(const int32_t* cu, int32_t nseq) {
+  int32_t m = 0;
+  for (int32_t s = 0; s < nseq; ++s) m = std::max(m, cu[s + 1] - cu[s]);
+  return m;
+}
+}  // namespace
+
 int qattn_qk_norm_rope(qattn_ctx* ctx, void* x, int64_t row_stride, int64_t col0, int32_t heads,
                        const int32_t* cu_seqlens, int32_t nseq, const float* weight, double eps,
                        double theta, qattn_stream_t stream) {
   if (!ctx || !x) return fail(ctx, QATTN_EINVAL, "ctx/x is NULL");
-  if (heads < 1 || col0 < 0 || row_stride < col0 + (int64_t)heads * kHeadDim)
-    return fail(ctx, QATTN_EINVAL, "bad heads/col0/row_stride (%d, %lld, %lld)", heads,
-                (long long)col0, (long long)row_stride);
+  if (heads < 4 || heads % 4 || heads > 32 || col0 < 0 || col0 % 8 || row_stride % 8 ||
+      row_stride < col0 + (int64_t)heads * kHeadDim)
+    return fail(ctx, QATTN_EINVAL, "bad heads/col0/row_stride (%d, %lld, %lld): heads a multiple of 4 in [4, 32], "
+                "col0 and row_stride multiples of 8", heads, (long long)col0, (long long)row_stride);
+  if (!aligned16(x) || (weight && reinterpret_cast<uintptr_t>(weight) % 16))
+    return fail(ctx, QATTN_EINVAL, "x must be 16-byte aligned (weight too)");
   if (!(eps >= 0.0) || !(theta > 0.0)) return fail(ctx, QATTN_EINVAL, "bad eps/theta");
   int rc = validate_cu(ctx, cu_seqlens, nseq);
   if (rc) return rc;
-  const int64_t T = cu_seqlens[nseq];
-  if (T == 0) return QATTN_OK;
-  int32_t maxlen = 0;
-  for (int32_t s = 0; s < nseq; ++s) maxlen = std::max(maxlen, cu_seqlens[s + 1] - cu_seqlens[s]);
-  // RoPE table exactly as model.ts:76-81: angle = pos * theta^(-i/64) in f64, cos/sin -> f32.
-  std::vector<float> table((size_t)maxlen * 128);
-  for (int32_t pos = 0; pos < maxlen; ++pos)
-    for (int i = 0; i < 64; ++i) {
-      const double angle = (double)pos * std::pow(theta, -(double)i / 64.0);
-      table[(size_t)pos * 64 + i] = (float)std::cos(angle);
-      table[(size_t)maxlen * 64 + (size_t)pos * 64 + i] = (float)std::sin(angle);
-    }
+  if (cu_seqlens[nseq] == 0) return QATTN_OK;
+  const float2* table = nullptr;
+  rc = rope_table(ctx, longest(cu_seqlens, nseq), theta, &table);
+  if (rc) return rc;
+  RopeArgs a{};
+  a.in = static_cast<const half_t*>(x);
+  a.out_q = a.out_k = static_cast<half_t*>(x) + col0;
+  a.weight_q = a.weight_k = weight;
+  a.rope = table;
+  a.in_stride = a.out_stride_q = a.out_stride_k = row_stride;
+  a.in_col_q = a.in_col_k = col0;
+  a.heads = a.split = heads;
+  a.eps = (float)eps;
   DeviceGuard g(ctx->device);
-  hipStream_t st = pick_stream(ctx, stream);
-  float* tab_dev = nullptr;
-  int32_t* cu_dev = nullptr;
-  HIP_TRY(ctx, hipMalloc(&tab_dev, table.size() * sizeof(float)));
-  hipError_t e = hipMalloc(&cu_dev, sizeof(int32_t) * (nseq + 1));
-  if (e == hipSuccess) e = hipMemcpyAsync(tab_dev, table.data(), table.size() * sizeof(float), hipMemcpyHostToDevice, st);
-  if (e == hipSuccess) e = hipMemcpyAsync(cu_dev, cu_seqlens, sizeof(int32_t) * (nseq + 1), hipMemcpyHostToDevice, st);
-  if (e == hipSuccess)
-    e = launch_qk_norm_rope(static_cast<half_t*>(x), row_stride, col0, heads, cu_dev, nseq, T, weight,
-                            eps, tab_dev, tab_dev + (size_t)maxlen * 64, st);
-  if (e == hipSuccess) e = hipStreamSynchronize(st);
-  (void)hipFree(tab_dev);
-  if (cu_dev) (void)hipFree(cu_dev);
-  if (e != hipSuccess) return fail(ctx, QATTN_EHIP, "qk_norm_rope: %s", hipGetErrorString(e));
+  HIP_TRY(ctx, launch_qk_norm_rope(a, cu_seqlens, nseq, pick_stream(ctx, stream)));
+  return QATTN_OK;
+}
+
+int qattn_qk_norm_rope_qkv(qattn_ctx* ctx, const void* qkv, int64_t qkv_row_stride, void* q,
+                           int64_t q_row_stride, void* k, int64_t k_row_stride,
+                           const int32_t* cu_seqlens, int32_t nseq, const float* q_weight,
+                           const float* k_weight, double eps, double theta, qattn_stream_t stream) {
+  if (!ctx || !qkv || !q || !k) return fail(ctx, QATTN_EINVAL, "ctx/qkv/q/k is NULL");
+  if (qkv_row_stride < 3072 || qkv_row_stride % 8 || q_row_stride < 2048 || q_row_stride % 8 ||
+      k_row_stride < 1024 || k_row_stride % 8)
+    return fail(ctx, QATTN_EINVAL, "strides (qkv %lld, q %lld, k %lld): >= 3072 / 2048 / 1024, multiples of 8",
+                (long long)qkv_row_stride, (long long)q_row_stride, (long long)k_row_stride);
+  if (!aligned16(qkv) || !aligned16(q) || !aligned16(k) ||
+      (q_weight && reinterpret_cast<uintptr_t>(q_weight) % 16) || (k_weight && reinterpret_cast<uintptr_t>(k_weight) % 16))
+    return fail(ctx, QATTN_EINVAL, "qkv/q/k (and weights) must be 16-byte aligned");
+  if (!(eps >= 0.0) || !(theta > 0.0)) return fail(ctx, QATTN_EINVAL, "bad eps/theta");
+  int rc = validate_cu(ctx, cu_seqlens, nseq);
+  if (rc) return rc;
+  if (cu_seqlens[nseq] == 0) return QATTN_OK;
+  const float2* table = nullptr;
+  rc = rope_table(ctx, longest(cu_seqlens, nseq), theta, &table);
+  if (rc) return rc;
+  RopeArgs a{};
+  a.in = static_cast<const half_t*>(qkv);
+  a.out_q = static_cast<half_t*>(q);
+  a.out_k = static_cast<half_t*>(k);
+  a.weight_q = q_weight;
+  a.weight_k = k_weight;
+  a.rope = table;
+  a.in_stride = qkv_row_stride;
+  a.out_stride_q = q_row_stride;
+  a.out_stride_k = k_row_stride;
+  a.in_col_q = 0;                   // Q block of the qkvRaw row (model.ts:69)
+  a.in_col_k = kQHeads * kHeadDim;  // K block
+  a.heads = kQHeads + kKVHeads;     // 24 head vectors per token (the reference's dispatch, ops.ts:158)
+  a.split = kQHeads;
+  a.eps = (float)eps;
+  DeviceGuard g(ctx->device);
+  HIP_TRY(ctx, launch_qk_norm_rope(a, cu_seqlens, nseq, pick_stream(ctx, stream)));
   return QATTN_OK;
 }
 

@@ -13,7 +13,8 @@ import numpy as np
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PKG_DIR)
-LIB_PATH = os.path.join(PKG_DIR, "libqattn.so")
+# QATTN_LIB selects another build of the same library (the sanitizer build of tests/sanitize.sh).
+LIB_PATH = os.environ.get("QATTN_LIB") or os.path.join(PKG_DIR, "libqattn.so")
 HEADER_PATH = os.path.join(REPO_DIR, "include", "qattn.h")
 
 OK, EINVAL, EHIP, ENOMEM, ENODEV = 0, -1, -2, -3, -4
@@ -99,6 +100,8 @@ def lib():
         "qattn_debug_run_mask": (ctypes.c_int, [vp, vp, i64, ctypes.POINTER(i32)]),
         "qattn_qk_norm_rope": (ctypes.c_int, [vp, vp, i64, i64, i32, vp, i32, vp,
                                               ctypes.c_double, ctypes.c_double, vp]),
+        "qattn_qk_norm_rope_qkv": (ctypes.c_int, [vp, vp, i64, vp, i64, vp, i64, vp, i32, vp, vp,
+                                                  ctypes.c_double, ctypes.c_double, vp]),
         "qattn_pool_last_l2": (ctypes.c_int, [vp, vp, i64, i32, vp, i32, vp, i64, vp]),
         "qattn_q4_compact_bytes": (i64, [i32, i32]),
         "qattn_q4_matmul": (ctypes.c_int, [vp, vp, i64, i32, i32, vp, i64, i32, vp, i64, vp]),
@@ -326,6 +329,14 @@ class Context:
         cu = np.ascontiguousarray(cu_seqlens, dtype=np.int32)
         _check(lib().qattn_qk_norm_rope(self.handle, x_ptr, row_stride, col0, heads, _np_ptr(cu),
                                         len(cu) - 1, weight_ptr, eps, theta, stream), self.handle)
+
+    def qk_norm_rope_qkv(self, qkv_ptr, q_ptr, k_ptr, cu_seqlens, qkv_row_stride=4096,
+                         q_row_stride=HQ * HD, k_row_stride=HKV * HD, q_weight_ptr=None,
+                         k_weight_ptr=None, eps=1e-6, theta=1e6, stream=None):
+        cu = np.ascontiguousarray(cu_seqlens, dtype=np.int32)
+        _check(lib().qattn_qk_norm_rope_qkv(self.handle, qkv_ptr, qkv_row_stride, q_ptr, q_row_stride,
+                                            k_ptr, k_row_stride, _np_ptr(cu), len(cu) - 1, q_weight_ptr,
+                                            k_weight_ptr, eps, theta, stream), self.handle)
 
     def pool_last_l2(self, x_ptr, row_stride, width, cu_seqlens, out_ptr, out_row_stride=None,
                      stream=None):

@@ -212,6 +212,87 @@ def test_qk_norm_rope_kernel_matches_oracle(ctx, oracle):
     buf.free()
 
 
+def _rope_compare(got, want, label):
+    diff = got != want
+    g, w = f16(got), f16(want)
+    ad = np.abs(g - w)
+    # One f16 step of the larger magnitude, and never less than the step at unit scale: f32 RMS
+    # and f32 (cos, sin) on the device against the oracle's f64 arithmetic move a result by at
+    # most one rounding step, in a few elements (outputs near zero stay within 2^-10 absolute).
+    step = np.maximum(2.0 ** -10, np.maximum(np.abs(g), np.abs(w)) * 2.0 ** -10)
+    print(f"{label}: {int(diff.sum())} of {diff.size} differ, max |d| {ad.max():.2e}, "
+          f"max |d|/step {(ad / step).max():.2f}", flush=True)
+    assert diff.mean() < 1e-2 and (ad <= step).all(), label
+
+
+def test_qk_norm_rope_in_place_q_block_with_gain(ctx, oracle):
+    rng = np.random.default_rng(13)
+    cu = cu_of([3, 64, 1, 129])
+    T = int(cu[-1])
+    x = (rng.standard_normal((T, 2048)) * 3).astype(np.float16).view(np.uint16)
+    w = (1 + 0.25 * rng.standard_normal(128)).astype(np.float32)
+    buf, bw = ctx.upload(x), ctx.upload(w)
+    ctx.qk_norm_rope(buf.ptr, 2048, 0, 16, cu, weight_ptr=bw.ptr)
+    got = buf.read(np.uint16, x.shape)
+    _rope_compare(got, oracle.qk_norm_rope(x.copy(), cu, heads=16, weight=w), "qk_norm_rope q gain")
+    for b in (buf, bw):
+        b.free()
+
+
+# (lengths, q row stride, k row stride): 70 sequences take two launches (64 per launch); 2100
+# positions grow the context's RoPE table past its first 1024 rows.
+ROPE_QKV_CASES = [
+    ([7, 1, 30], 2048, 1024),
+    ([500] * 4, 2048 + 64, 1024 + 8),
+    ([1 + (i * 37) % 50 for i in range(70)], 2048, 1024),
+    ([2100, 5], 2048, 1024),
+]
+
+
+@pytest.mark.parametrize("lengths,qs,ks", ROPE_QKV_CASES)
+def test_qk_norm_rope_qkv_matches_oracle(ctx, oracle, lengths, qs, ks):
+    """The fused producer: qkvRaw [T, 4096] -> compact Q and K, each block with its own gain, the
+    V block and qkvRaw itself untouched (QKNormRopeKernel, ops.ts:104-166)."""
+    rng = np.random.default_rng(len(lengths) * 1000 + qs)
+    cu = cu_of(lengths)
+    T = int(cu[-1])
+    x = (rng.standard_normal((T, 4096)) * 2).astype(np.float16).view(np.uint16)
+    wq = (1 + 0.25 * rng.standard_normal(128)).astype(np.float32)
+    wk = (1 + 0.25 * rng.standard_normal(128)).astype(np.float32)
+    bx, bwq, bwk = ctx.upload(x), ctx.upload(wq), ctx.upload(wk)
+    bq, bk = ctx.alloc(T * qs * 2), ctx.alloc(T * ks * 2)
+    sentinel = 0x7BFF
+    bq.fill_u16(sentinel)
+    bk.fill_u16(sentinel)
+    ctx.qk_norm_rope_qkv(bx.ptr, bq.ptr, bk.ptr, cu, q_row_stride=qs, k_row_stride=ks,
+                         q_weight_ptr=bwq.ptr, k_weight_ptr=bwk.ptr)
+    got_q = bq.read(np.uint16, (T, qs))
+    got_k = bk.read(np.uint16, (T, ks))
+    assert np.array_equal(bx.read(np.uint16, x.shape), x)
+    assert (got_q[:, 2048:] == sentinel).all() and (got_k[:, 1024:] == sentinel).all()
+    want_q = oracle.qk_norm_rope(np.ascontiguousarray(x[:, :2048]), cu, heads=16, weight=wq)
+    want_k = oracle.qk_norm_rope(np.ascontiguousarray(x[:, 2048:3072]), cu, heads=8, weight=wk)
+    _rope_compare(got_q[:, :2048], want_q, f"qkv producer Q {len(lengths)} seqs")
+    _rope_compare(got_k[:, :1024], want_k, f"qkv producer K {len(lengths)} seqs")
+    for b in (bx, bwq, bwk, bq, bk):
+        b.free()
+
+
+def test_qk_norm_rope_rejects_bad_layouts(ctx, qattn):
+    buf = ctx.alloc(64 * 4096 * 2)
+    cu = cu_of([64])
+    for kw in ({"heads": 6}, {"heads": 0}, {"col0": 4}, {"row_stride": 4092}):
+        a = {"row_stride": 4096, "col0": 0, "heads": 8}
+        a.update(kw)
+        with pytest.raises(qattn.QattnError):
+            ctx.qk_norm_rope(buf.ptr, a["row_stride"], a["col0"], a["heads"], cu)
+    with pytest.raises(qattn.QattnError):
+        ctx.qk_norm_rope_qkv(buf.ptr + 2, buf.ptr, buf.ptr, cu)
+    with pytest.raises(qattn.QattnError):
+        ctx.qk_norm_rope_qkv(buf.ptr, buf.ptr, buf.ptr, cu, q_row_stride=2040)
+    buf.free()
+
+
 def _exact_and_gpu(ctx, qattn, oracle, lengths, config=0, mask=1, P=176, W=432, rows=None, **kw):
     cu = cu_of(lengths)
     q, k, v = oracle.gen_qkv(config, 0, cu)
