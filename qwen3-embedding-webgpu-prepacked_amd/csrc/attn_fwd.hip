@@ -259,18 +259,29 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   // key = kb + 4*hl + key_off(r), r = 0..31 over (s[0], s[1]).
   // `step_hook(st)` runs after step st's MFMAs (the main loop issues its tile loads there, one
   // per step, so they reach the texture unit spread out instead of in one burst per iteration).
+  // Each step's K fragments are read one step ahead, before the previous step's tile load (which
+  // the compiler may not move LDS reads across), so no MFMA waits for its own LDS read.
   auto qk = [&](const char* kt, f16x (&s)[2], auto step_hook) {
     uint32_t kx = kread_xor;
     asm volatile("" : "+v"(kx));  // keeps the 8 addresses from being hoisted into registers
+    auto frag = [&](int st, int half) {
+      const uint32_t ka = kread_base + (((uint32_t)st << 5) ^ kx) + half * 32 * kRowBytes;
+      return *reinterpret_cast<const h8*>(kt + ka);
+    };
+    h8 a0 = frag(0, 0), a1 = frag(0, 1);
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
-      const uint32_t ka = kread_base + (((uint32_t)st << 5) ^ kx);
-      const h8 a0 = *reinterpret_cast<const h8*>(kt + ka);
-      const h8 a1 = *reinterpret_cast<const h8*>(kt + ka + 32 * kRowBytes);
+      h8 n0 = a0, n1 = a1;
+      if (st < 7) {
+        n0 = frag(st + 1, 0);
+        n1 = frag(st + 1, 1);
+      }
       // step 0 accumulates onto the inline constant 0 (no zeroed registers)
       s[0] = mfma32(a0, qreg[st], st == 0 ? f16x{} : s[0]);
       s[1] = mfma32(a1, qreg[st], st == 0 ? f16x{} : s[1]);
       step_hook(st);
+      a0 = n0;
+      a1 = n1;
     }
   };
   auto no_hook = [](int) {};
