@@ -129,6 +129,14 @@ int qattn_run_encode(qattn_run* run, qattn_stream_t stream);
 /* Re-points a run at other tensors of the same shape (layers sharing one packing). */
 int qattn_run_rebind(qattn_run* run, const void* q, const void* k, const void* v, void* o,
                      void* o_last);
+/* Re-plans a run for new sequence lengths: same tensors, strides, mask and flags, new cu_seqlens
+ * (validated as by qattn_run_create).  The reference creates a run per (batch, sequence) plan
+ * shape and rebuilds its uniforms per batch (embedding-engine.ts:70-75, ops.ts:327-343); a
+ * varlen batch changes the work list, so one run kept at capacity takes every batch of a plan.
+ * Waits for the device to be idle (launches of the previous plan may still read its work list),
+ * uploads the new work list, and allocates device memory only when the work list or the split
+ * workspace outgrows every earlier one.  The tensors must hold the new token count. */
+int qattn_run_update(qattn_run* run, const int32_t* cu_seqlens, int32_t nseq);
 void qattn_run_destroy(qattn_run* run);
 
 typedef struct qattn_run_info {

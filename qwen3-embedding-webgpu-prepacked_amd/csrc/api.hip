@@ -66,11 +66,12 @@ struct qattn_ctx {
 struct qattn_run {
   qattn_ctx* ctx = nullptr;
   AttnParams params{};
-  void* plan_dev = nullptr;  // work items by slot, then the slot offsets
-  void* split_dev = nullptr; // the chunks' partial results (merged by a second kernel)
-  int64_t v_offset = 0;
-  int32_t max_len = 0;  // longest sequence
-  bool has_o_last = false;
+  void* plan_dev = nullptr;   // the plan image (work list, tile list, slot offsets)
+  void* split_dev = nullptr;  // the chunks' partial results (merged by a second kernel)
+  size_t plan_capacity = 0;   // bytes at plan_dev
+  int32_t partial_capacity = 0;  // partial-result records at split_dev
+  qattn_run_desc desc{};      // the description it was created with (cu_seqlens: not kept)
+  int32_t max_len = 0;        // longest sequence
   qattn_run_info info{};
 };
 
@@ -338,63 +339,104 @@ int qattn_plan_slots(const qattn_run_desc* desc, int32_t max_slots, int32_t* slo
   return QATTN_OK;
 }
 
-int qattn_run_create(qattn_ctx* ctx, const qattn_run_desc* d, qattn_run** out) {
-  if (!ctx || !out) return fail(ctx, QATTN_EINVAL, "ctx/out is NULL");
-  *out = nullptr;
+}  // extern "C"
+
+namespace {
+
+// Plans a validated description into `run`: the work list goes to the run's device buffer and
+// the split workspace is sized for it, both reallocated only when they must grow.  The device
+// must not be running a launch of the run's previous plan.
+int install_plan(qattn_run* run, const qattn_run_desc* d) {
+  qattn_ctx* ctx = run->ctx;
   Plan plan;
   qattn_run_info info{};
   MaskSpec mask{};
-  int rc = validate_desc(ctx, d);
-  if (rc) return rc;
   plan_work(d, std::max(1, ctx->cu_count) * kBlocksPerCU, &plan, &info, &mask);
-
-  auto* run = new (std::nothrow) qattn_run();
-  if (!run) return fail(ctx, QATTN_ENOMEM, "out of host memory");
-  run->ctx = ctx;
-  run->info = info;
-  run->v_offset = d->v_offset;
-  run->has_o_last = d->o_last != nullptr;
-  for (int32_t s = 0; s < d->nseq; ++s) run->max_len = std::max(run->max_len, d->cu_seqlens[s + 1] - d->cu_seqlens[s]);
   // One upload: the entries, the split items' chunk-0 entries, then the slot offsets (32-byte
   // entries keep the offsets aligned).
   const size_t items_bytes = plan.items.size() * sizeof(WorkItem);
   const size_t heads_bytes = plan.split_heads.size() * sizeof(WorkItem);
   const size_t slots_bytes = plan.slot_begin.size() * sizeof(int32_t);
-  std::vector<char> host(items_bytes + heads_bytes + slots_bytes);
-  if (items_bytes) std::memcpy(host.data(), plan.items.data(), items_bytes);
-  if (heads_bytes) std::memcpy(host.data() + items_bytes, plan.split_heads.data(), heads_bytes);
-  std::memcpy(host.data() + items_bytes + heads_bytes, plan.slot_begin.data(), slots_bytes);
-  {
-    DeviceGuard g(ctx->device);
-    hipError_t e = hipMalloc(&run->plan_dev, host.size());
-    if (e != hipSuccess) {
-      delete run;
-      return fail(ctx, QATTN_ENOMEM, "hipMalloc(work list): %s", hipGetErrorString(e));
-    }
-    e = hipMemcpy(run->plan_dev, host.data(), host.size(), hipMemcpyHostToDevice);
-    if (e != hipSuccess) {
-      (void)hipFree(run->plan_dev);
-      delete run;
-      return fail(ctx, QATTN_EHIP, "hipMemcpy(work list): %s", hipGetErrorString(e));
-    }
+  std::vector<char> image(items_bytes + heads_bytes + slots_bytes);
+  if (items_bytes) std::memcpy(image.data(), plan.items.data(), items_bytes);
+  if (heads_bytes) std::memcpy(image.data() + items_bytes, plan.split_heads.data(), heads_bytes);
+  std::memcpy(image.data() + items_bytes + heads_bytes, plan.slot_begin.data(), slots_bytes);
+  DeviceGuard g(ctx->device);
+  if (image.size() > run->plan_capacity) {
+    if (run->plan_dev) (void)hipFree(run->plan_dev);
+    run->plan_dev = nullptr;
+    run->plan_capacity = 0;
+    hipError_t e = hipMalloc(&run->plan_dev, image.size());
+    if (e != hipSuccess) return fail(ctx, QATTN_ENOMEM, "hipMalloc(work list): %s", hipGetErrorString(e));
+    run->plan_capacity = image.size();
   }
-  // Split items: the chunks' partial results.
-  if (plan.splits) {
-    DeviceGuard g(ctx->device);
-    hipError_t e = hipMalloc(&run->split_dev, (size_t)plan.partials * kPartialBytes);
-    if (e != hipSuccess) {
-      if (run->split_dev) (void)hipFree(run->split_dev);
-      (void)hipFree(run->plan_dev);
-      delete run;
+  hipError_t e = hipMemcpy(run->plan_dev, image.data(), image.size(), hipMemcpyHostToDevice);
+  if (e != hipSuccess) return fail(ctx, QATTN_EHIP, "hipMemcpy(work list): %s", hipGetErrorString(e));
+  if (plan.partials > run->partial_capacity) {
+    if (run->split_dev) (void)hipFree(run->split_dev);
+    run->split_dev = nullptr;
+    run->partial_capacity = 0;
+    e = hipMalloc(&run->split_dev, (size_t)plan.partials * kPartialBytes);
+    if (e != hipSuccess)
       return fail(ctx, QATTN_ENOMEM, "split workspace (%d chunks): %s", plan.partials, hipGetErrorString(e));
-    }
+    run->partial_capacity = plan.partials;
   }
-  AttnParams& p = run->params;
-  fill_params(&p, d, mask, info.slots, run->plan_dev, items_bytes, heads_bytes);
-  p.partials = static_cast<float*>(run->split_dev);
-  p.n_splits = plan.splits;
+  fill_params(&run->params, d, mask, info.slots, run->plan_dev, items_bytes, heads_bytes);
+  run->params.partials = static_cast<float*>(run->split_dev);
+  run->params.n_splits = plan.splits;
+  run->info = info;
+  run->max_len = 0;
+  for (int32_t s = 0; s < d->nseq; ++s) run->max_len = std::max(run->max_len, d->cu_seqlens[s + 1] - d->cu_seqlens[s]);
+  run->desc = *d;
+  run->desc.cu_seqlens = nullptr;
+  run->desc.nseq = 0;
+  return QATTN_OK;
+}
+
+void free_run(qattn_run* run) {
+  if (run->plan_dev || run->split_dev) {
+    DeviceGuard g(run->ctx->device);
+    (void)hipStreamSynchronize(run->ctx->stream);
+    if (run->plan_dev) (void)hipFree(run->plan_dev);
+    if (run->split_dev) (void)hipFree(run->split_dev);
+  }
+  delete run;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qattn_run_create(qattn_ctx* ctx, const qattn_run_desc* d, qattn_run** out) {
+  if (!ctx || !out) return fail(ctx, QATTN_EINVAL, "ctx/out is NULL");
+  *out = nullptr;
+  int rc = validate_desc(ctx, d);
+  if (rc) return rc;
+  auto* run = new (std::nothrow) qattn_run();
+  if (!run) return fail(ctx, QATTN_ENOMEM, "out of host memory");
+  run->ctx = ctx;
+  rc = install_plan(run, d);
+  if (rc) {
+    free_run(run);
+    return rc;
+  }
   *out = run;
   return QATTN_OK;
+}
+
+int qattn_run_update(qattn_run* run, const int32_t* cu_seqlens, int32_t nseq) {
+  if (!run) return fail(nullptr, QATTN_EINVAL, "run is NULL");
+  qattn_run_desc d = run->desc;
+  d.cu_seqlens = cu_seqlens;
+  d.nseq = nseq;
+  int rc = validate_desc(run->ctx, &d);
+  if (rc) return rc;
+  {
+    // Launches of the previous plan (on any stream) may still read its work list.
+    DeviceGuard g(run->ctx->device);
+    HIP_TRY(run->ctx, hipDeviceSynchronize());
+  }
+  return install_plan(run, &d);
 }
 
 int qattn_run_encode(qattn_run* run, qattn_stream_t stream) {
@@ -412,26 +454,24 @@ int qattn_run_rebind(qattn_run* run, const void* q, const void* k, const void* v
   if (!q || !k || !v || !o) return fail(run->ctx, QATTN_EINVAL, "q/k/v/o must be non-NULL");
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || (o_last && !aligned16(o_last)))
     return fail(run->ctx, QATTN_EINVAL, "q/k/v/o/o_last must be 16-byte aligned");
-  if ((o_last != nullptr) != run->has_o_last)
+  if ((o_last != nullptr) != (run->desc.o_last != nullptr))
     return fail(run->ctx, QATTN_EINVAL, "o_last presence must match the run's description");
   AttnParams& p = run->params;
   p.q = static_cast<const half_t*>(q);
   p.k = static_cast<const half_t*>(k);
-  p.v = static_cast<const half_t*>(v) + run->v_offset;
+  p.v = static_cast<const half_t*>(v) + run->desc.v_offset;
   p.o = static_cast<half_t*>(o);
   p.o_last = static_cast<half_t*>(o_last);
+  run->desc.q = q;
+  run->desc.k = k;
+  run->desc.v = v;
+  run->desc.o = o;
+  run->desc.o_last = o_last;
   return QATTN_OK;
 }
 
 void qattn_run_destroy(qattn_run* run) {
-  if (!run) return;
-  if (run->plan_dev || run->split_dev) {
-    DeviceGuard g(run->ctx->device);
-    (void)hipStreamSynchronize(run->ctx->stream);
-    if (run->plan_dev) (void)hipFree(run->plan_dev);
-    if (run->split_dev) (void)hipFree(run->split_dev);
-  }
-  delete run;
+  if (run) free_run(run);
 }
 
 int qattn_run_get_info(const qattn_run* run, qattn_run_info* info) {

@@ -9,6 +9,8 @@
 // the engine's run() stays asynchronous like the reference's mapAsync readback (model.ts:135).
 #include <node_api.h>
 
+#include <algorithm>
+#include <climits>
 #include <cstdint>
 #include <cstring>
 #include <set>
@@ -50,9 +52,16 @@ struct Buf {
   void* ptr = nullptr;
   size_t bytes = 0;
 };
+// A run holds a reference on each buffer bound to it (so none is collected before the run), and
+// the largest token / sequence counts those buffers can take (updateRun checks new batches
+// against them).
 struct Run {
   Ctx* owner = nullptr;
   qattn_run* run = nullptr;
+  std::vector<napi_ref> bound_refs;
+  std::vector<const Buf*> bound;
+  int64_t max_tokens = 0;
+  int64_t max_seqs = 0;  // o_last rows (no limit without o_last)
 };
 
 void release_device(Ctx* c);
@@ -153,10 +162,16 @@ void finalize_buf(napi_env, void* data, void*) {
   delete b;
   unref(c);
 }
-void finalize_run(napi_env, void* data, void*) {
+void drop_bound(napi_env env, Run* r) {
+  for (napi_ref ref : r->bound_refs) napi_delete_reference(env, ref);
+  r->bound_refs.clear();
+  r->bound.clear();
+}
+void finalize_run(napi_env env, void* data, void*) {
   auto* r = static_cast<Run*>(data);
   Ctx* c = r->owner;
   if (r->run && c->ctx) qattn_run_destroy(r->run);
+  drop_bound(env, r);
   c->runs.erase(r);
   delete r;
   unref(c);
@@ -339,15 +354,19 @@ bool get_i32_array(napi_env env, napi_value v, std::vector<int32_t>* out) {
 // context `owner` with optional byte offsets (qOffsetBytes, ...), strides in elements.  With a
 // device, every tensor's extent -- the bytes the kernels can touch, from its offset, strides and
 // the token count -- is checked against its buffer (RangeError), as WebGPU validates bindings.
+struct Binding {
+  const Buf* buf = nullptr;
+  int64_t off = 0;
+  napi_value js = nullptr;
+};
+struct Bindings {
+  Binding q, k, v, o, last;
+};
 bool read_desc(napi_env env, napi_value d, qattn_run_desc* desc, std::vector<int32_t>* cu,
-               const Ctx* owner) {
+               const Ctx* owner, Bindings* bindings = nullptr) {
   const bool need_device = owner != nullptr;
   std::memset(desc, 0, sizeof(*desc));
   napi_value v;
-  struct Binding {
-    const Buf* buf = nullptr;
-    int64_t off = 0;
-  };
   auto ptr_of = [&](const char* name, const char* off_name, const void** out, bool required,
                     Binding* bind) {
     if (!prop(env, d, name, &v)) {
@@ -376,10 +395,13 @@ bool read_desc(napi_env env, napi_value d, qattn_run_desc* desc, std::vector<int
     *out = static_cast<const char*>(b->ptr) + off;
     bind->buf = b;
     bind->off = off;
+    bind->js = v;
     return true;
   };
   const void *q, *k, *vv, *o, *ol = nullptr;
-  Binding bq, bk, bv, bo, bl;
+  Bindings local;
+  Bindings& bb = bindings ? *bindings : local;
+  Binding &bq = bb.q, &bk = bb.k, &bv = bb.v, &bo = bb.o, &bl = bb.last;
   if (!ptr_of("q", "qOffsetBytes", &q, true, &bq) || !ptr_of("k", "kOffsetBytes", &k, true, &bk) ||
       !ptr_of("v", "vOffsetBytes", &vv, true, &bv) || !ptr_of("o", "oOffsetBytes", &o, true, &bo) ||
       !ptr_of("oLast", "oLastOffsetBytes", &ol, false, &bl))
@@ -463,11 +485,28 @@ napi_value CreateRun(napi_env env, napi_callback_info info) {
   if (!c) return nullptr;
   qattn_run_desc desc;
   std::vector<int32_t> cu;
-  if (!read_desc(env, argv[1], &desc, &cu, c)) return nullptr;
+  Bindings bind;
+  if (!read_desc(env, argv[1], &desc, &cu, c, &bind)) return nullptr;
   qattn_run* run = nullptr;
   int rc = qattn_run_create(c->ctx, &desc, &run);
   if (rc) return throw_qattn(env, rc, c->ctx);
   auto* r = new Run{c, run};
+  // Capacity: the most rows every bound tensor can hold at its offset and stride.
+  auto rows_fit = [](const Binding& b, int64_t stride, int64_t extra, int64_t width) {
+    const int64_t avail = (int64_t)b.buf->bytes / 2 - b.off / 2 - extra - width;
+    return avail < 0 ? 0 : avail / std::max<int64_t>(stride, 1) + 1;
+  };
+  r->max_tokens = std::min(std::min(rows_fit(bind.q, desc.q_row_stride, 0, 2048), rows_fit(bind.k, desc.k_row_stride, 0, 1024)),
+                           std::min(rows_fit(bind.v, desc.v_row_stride, desc.v_offset, 1024),
+                                    rows_fit(bind.o, desc.o_row_stride, 0, 2048)));
+  r->max_seqs = desc.o_last ? (int64_t)(bind.last.buf->bytes - bind.last.off) / 4096 : INT64_MAX;
+  for (const Binding* b : {&bind.q, &bind.k, &bind.v, &bind.o, &bind.last}) {
+    if (!b->buf) continue;
+    napi_ref ref;
+    NAPI_OK(env, napi_create_reference(env, b->js, 1, &ref));
+    r->bound_refs.push_back(ref);
+    r->bound.push_back(b->buf);
+  }
   c->runs.insert(r);
   ++c->refs;
   napi_value out;
@@ -481,7 +520,33 @@ Run* live_run(napi_env env, napi_value v) {
     napi_throw_error(env, nullptr, r->run ? "context was destroyed" : "attention run was destroyed");
     return nullptr;
   }
+  if (r)
+    for (const Buf* b : r->bound)
+      if (!b->ptr) {
+        napi_throw_error(env, nullptr, "a device buffer bound to this run was freed");
+        return nullptr;
+      }
   return r;
+}
+
+// updateRun(run, cuSeqlens)  -- a new batch for the same tensors (qattn_run_update)
+napi_value UpdateRun(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!args_of(env, info, 2, argv)) return nullptr;
+  Run* r = live_run(env, argv[0]);
+  if (!r) return nullptr;
+  std::vector<int32_t> cu;
+  if (!get_i32_array(env, argv[1], &cu) || cu.size() < 2) {
+    napi_throw_type_error(env, nullptr, "cuSeqlens must be an Int32Array of nseq+1 offsets");
+    return nullptr;
+  }
+  if ((int64_t)cu.back() > r->max_tokens || (int64_t)cu.size() - 1 > r->max_seqs) {
+    napi_throw_range_error(env, nullptr, "the batch exceeds the buffers bound to this run");
+    return nullptr;
+  }
+  int rc = qattn_run_update(r->run, cu.data(), (int32_t)cu.size() - 1);
+  if (rc) return throw_qattn(env, rc, r->owner->ctx);
+  return undefined(env);
 }
 
 // encode(run)  (reference: CausalAttentionKernel.encode(pass, run))
@@ -502,6 +567,7 @@ napi_value DestroyRun(napi_env env, napi_callback_info info) {
   if (!r) return nullptr;
   if (r->run && r->owner->ctx) qattn_run_destroy(r->run);
   r->run = nullptr;
+  drop_bound(env, r);
   return undefined(env);
 }
 
@@ -617,7 +683,8 @@ napi_value FillTokenRows(napi_env env, napi_callback_info info) {
     napi_throw_type_error(env, nullptr, "expected numbers");
     return nullptr;
   }
-  if ((size_t)rows * 4 > ids->bytes || (size_t)(rows * stride) * 2 > dst->bytes) {
+  if (rows < 0 || elems < 0 || elems > stride || (size_t)rows * 4 > ids->bytes ||
+      (rows > 0 && (size_t)((rows - 1) * stride + elems) * 2 > dst->bytes)) {
     napi_throw_range_error(env, nullptr, "rows exceed the buffers");
     return nullptr;
   }
@@ -629,6 +696,41 @@ napi_value FillTokenRows(napi_env env, napi_callback_info info) {
 }
 
 // qkNormRope(ctx, x, rowStride, col0, heads, cuSeqlens, eps, theta)
+// qkNormRopeQkv(ctx, qkv, qkvStride, q, qStride, k, kStride, cuSeqlens, eps, theta)
+// (reference: QKNormRopeKernel.createRun + dispatch, ops.ts:104-166; unit gains)
+napi_value QkNormRopeQkv(napi_env env, napi_callback_info info) {
+  napi_value argv[10];
+  if (!args_of(env, info, 10, argv)) return nullptr;
+  Ctx* c = live_ctx(env, argv[0]);
+  if (!c) return nullptr;
+  Buf* qkv = live_buf(env, argv[1]);
+  Buf* q = qkv ? live_buf(env, argv[3]) : nullptr;
+  Buf* k = q ? live_buf(env, argv[5]) : nullptr;
+  if (!k) return nullptr;
+  int64_t s_qkv, s_q, s_k;
+  double eps = 1e-6, theta = 1e6;
+  std::vector<int32_t> cu;
+  if (!get_i64(env, argv[2], &s_qkv) || !get_i64(env, argv[4], &s_q) || !get_i64(env, argv[6], &s_k) ||
+      !get_i32_array(env, argv[7], &cu) || cu.size() < 2 || napi_get_value_double(env, argv[8], &eps) != napi_ok ||
+      napi_get_value_double(env, argv[9], &theta) != napi_ok) {
+    napi_throw_type_error(env, nullptr,
+                          "expected (ctx, qkv, qkvStride, q, qStride, k, kStride, cuSeqlens, eps, theta)");
+    return nullptr;
+  }
+  const int64_t T = cu.back();
+  auto fits = [&](const Buf* b, int64_t stride, int64_t width) {
+    return stride >= width && (T <= 0 || (uint64_t)((T - 1) * stride + width) * 2 <= b->bytes);
+  };
+  if (!fits(qkv, s_qkv, 3072) || !fits(q, s_q, 2048) || !fits(k, s_k, 1024)) {
+    napi_throw_range_error(env, nullptr, "rows x stride exceed a device buffer");
+    return nullptr;
+  }
+  int rc = qattn_qk_norm_rope_qkv(c->ctx, qkv->ptr, s_qkv, q->ptr, s_q, k->ptr, s_k, cu.data(),
+                                  (int32_t)cu.size() - 1, nullptr, nullptr, eps, theta, nullptr);
+  if (rc) return throw_qattn(env, rc, c->ctx);
+  return undefined(env);
+}
+
 napi_value QkNormRope(napi_env env, napi_callback_info info) {
   napi_value argv[8];
   if (!args_of(env, info, 8, argv)) return nullptr;
@@ -784,6 +886,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"planDescribe", PlanDescribe}, {"planMask", PlanMask},
       {"debugMask", DebugMask},       {"genQkv", GenQkv},
       {"fillTokenRows", FillTokenRows}, {"qkNormRope", QkNormRope},
+      {"qkNormRopeQkv", QkNormRopeQkv}, {"updateRun", UpdateRun},
       {"poolLastL2", PoolLastL2},     {"q4Matmul", Q4Matmul},
       {"synchronize", Synchronize},   {"synchronizeAsync", SynchronizeAsync},
   };

@@ -5,7 +5,8 @@
 //             valueOffset = 0) -> AttentionRun      (padded [batch, sequence] layout, ops.ts:327)
 //   encode(run)                                     (ops.ts:344; the stream is the context's)
 //   destroyRun(run)                                 (the run's owned buffers, model.ts:108-111)
-// plus createVarlenRun(q, k, v, output, cuSeqlens, options) for packed sequences.
+// plus createVarlenRun(q, k, v, output, cuSeqlens, options) for packed sequences and
+// updateRun(run, cuSeqlens) to re-plan a run for the next batch of the same tensors.
 // Buffers are device buffers from DeviceContext.alloc().  The mask is the reference's
 // always-on 176-token prefix + 432-token local window (ops.ts:206) unless options say otherwise.
 
@@ -80,6 +81,15 @@ class CausalAttentionKernel {
     const addon = this.context.addon;
     const handle = addon.createRun(this.context.handle, desc);
     return { handle, info: addon.runInfo(handle), cuSeqlens: desc.cuSeqlens };
+  }
+
+  // A new batch for a run's tensors: re-plans the work list in place (qattn_run_update), so one
+  // run created at a plan's capacity serves every batch of that plan.
+  updateRun(run, cuSeqlens) {
+    const cu = Int32Array.from(cuSeqlens);
+    this.context.addon.updateRun(run.handle, cu);
+    run.cuSeqlens = cu;
+    run.info = this.context.addon.runInfo(run.handle);
   }
 
   encode(run) { this.context.addon.encode(run.handle); }

@@ -87,6 +87,7 @@ def lib():
         "qattn_run_create": (ctypes.c_int, [vp, ctypes.POINTER(RunDesc), pvp]),
         "qattn_run_encode": (ctypes.c_int, [vp, vp]),
         "qattn_run_rebind": (ctypes.c_int, [vp, vp, vp, vp, vp, vp]),
+        "qattn_run_update": (ctypes.c_int, [vp, vp, i32]),
         "qattn_run_destroy": (None, [vp]),
         "qattn_run_get_info": (ctypes.c_int, [vp, ctypes.POINTER(RunInfo)]),
         "qattn_plan_describe": (ctypes.c_int, [ctypes.POINTER(RunDesc), vp, i32,
@@ -220,6 +221,11 @@ class Run:
 
     def rebind(self, q, k, v, o, o_last=None):
         _check(lib().qattn_run_rebind(self.handle, q, k, v, o, o_last), self.ctx.handle)
+
+    def update(self, cu_seqlens):
+        """Re-plan for new sequence lengths (qattn_run_update); same tensors and options."""
+        cu = np.ascontiguousarray(cu_seqlens, dtype=np.int32)
+        _check(lib().qattn_run_update(self.handle, _np_ptr(cu), len(cu) - 1), self.ctx.handle)
 
     def info(self):
         i = RunInfo()

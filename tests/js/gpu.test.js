@@ -166,6 +166,62 @@ test('.wgpack compact Q4_0 tensor -> device -> CompactQ4Matmul equals the host p
   for (const b of [x, y, weight.buffer]) b.destroy();
 });
 
+test('a plan re-plans its one attention run per batch: same results as a fresh plan, any lengths', async () => {
+  const runtime = new HipAttentionRuntime({ context: ctx, layers: 2 });
+  const plan = runtime.createPlan(4, 300);
+  const handle = plan.attentionRun.handle;
+  const batches = [[300, 300, 300, 300], [1, 2, 3, 4], [299, 17, 300, 64], [5, 300, 1, 250]];
+  for (const lengths of batches) {
+    const total = lengths.reduce((a, b) => a + b, 0);
+    const ids = Uint32Array.from({ length: total }, (_, i) => (i * 7919 + lengths[0]) % 151000);
+    const got = await plan.run(ids, lengths);
+    assert.strictEqual(plan.attentionRun.handle, handle);
+    assert.strictEqual(plan.attentionRun.info.tokens, total);
+    const fresh = runtime.createPlan(4, Math.max.apply(null, lengths));
+    const want = await fresh.run(ids, lengths);
+    for (let i = 0; i < 4; i += 1) assert.deepStrictEqual(Array.from(got[i]), Array.from(want[i]), `${lengths} request ${i}`);
+    fresh.destroy();
+    runtime.plans.pop();
+  }
+  assert.throws(() => runtime.attention.updateRun(plan.attentionRun, [0, 1201]), RangeError);
+  plan.destroy();
+  runtime.plans = [];
+});
+
+test('host enqueue time of one 16 x 500 batch, 28 layers (reported)', async () => {
+  const runtime = new HipAttentionRuntime({ context: ctx, layers: 28 });
+  const plan = runtime.createPlan(16, 500);
+  const lengths = new Uint32Array(16).fill(500);
+  const ids = Uint32Array.from({ length: 8000 }, (_, i) => (i * 104729) % 151000);
+  await plan.run(ids, lengths);  // warm
+  const runs = [];
+  for (let r = 0; r < 5; r += 1) {
+    await plan.run(ids, lengths);
+    runs.push(plan.timing);
+  }
+  const med = (key) => runs.map((t) => t[key]).sort((a, b) => a - b)[2];
+  console.log(`# embed host timing: ${JSON.stringify({ batch: '16x500', layers: 28, launches: 28 * 3 + 1,
+    host_enqueue_ms: +med('hostMs').toFixed(3), wall_ms: +med('totalMs').toFixed(3),
+    host_us_per_launch: +(1000 * med('hostMs') / (28 * 3 + 1)).toFixed(2) })}`);
+  assert.ok(med('hostMs') < med('totalMs'));
+  plan.destroy();
+  runtime.plans = [];
+});
+
+test('a run whose bound buffer was freed refuses to encode or re-plan', () => {
+  const attention = new CausalAttentionKernel(ctx);
+  const T = 64;
+  const bufs = [ctx.alloc(T * 4096), ctx.alloc(T * 2048), ctx.alloc(T * 2048), ctx.alloc(T * 4096)];
+  const run = attention.createVarlenRun(bufs[0], bufs[1], bufs[2], bufs[3], [0, T], { mask: 'causal' });
+  attention.encode(run);
+  ctx.synchronize();
+  bufs[2].destroy();
+  assert.throws(() => attention.encode(run), /freed/);
+  assert.throws(() => attention.updateRun(run, [0, 32]), /freed/);
+  attention.destroyRun(run);
+  for (const b of bufs) b.destroy();
+});
+
 test('plan.run rejects malformed input before launching', async () => {
   const runtime = new HipAttentionRuntime({ context: ctx, layers: 1 });
   const plan = runtime.createPlan(2, 4);

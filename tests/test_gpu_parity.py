@@ -443,6 +443,46 @@ def test_run_reuse_rebind_and_determinism(ctx, qattn, oracle):
     compare(rebound[::7], exact, "16x500-style layer 1 sampled")
 
 
+@pytest.mark.parametrize("flags", [0, 1])
+def test_run_update_replans_in_place(ctx, qattn, oracle, flags):
+    """qattn_run_update: one run at capacity takes batches of other lengths -- smaller, larger
+    work lists (the device buffers grow), split items and back -- bit for bit what a fresh run of
+    each batch computes; a rejected update leaves the run usable."""
+    cap = 5000
+    bq, bk, bv = ctx.alloc(cap * 4096), ctx.alloc(cap * 2048), ctx.alloc(cap * 2048)
+    bo, bl = ctx.alloc(cap * 4096), ctx.alloc(64 * 4096)
+    cu0 = cu_of([7])
+    run = ctx.run(qattn.make_desc(bq.ptr, bk.ptr, bv.ptr, bo.ptr, cu0, o_last=bl.ptr, flags=flags))
+    batches = [[500] * 4, [5000], [1, 609, 64, 177, 1500, 2], [33], [4000, 1000], [120] * 40]
+    for lengths in batches:
+        cu = cu_of(lengths)
+        T = int(cu[-1])
+        q, k, v = oracle.gen_qkv(1, len(lengths), cu)
+        bq.write(q)
+        bk.write(k)
+        bv.write(v)
+        run.update(cu)
+        info = run.info()
+        assert info.tokens == T
+        run.encode()
+        ctx.synchronize()
+        got = bo.read(np.uint16, (T, 2048))
+        got_last = bl.read(np.uint16, (len(lengths), 2048))
+        fresh = Case(ctx, qattn, q, k, v, cu, o_last=True, flags=flags)
+        want = fresh.run()
+        print(f"update {lengths[:4]}{'...' if len(lengths) > 4 else ''}: slots {info.slots}, "
+              f"split items {info.split_items}", flush=True)
+        assert np.array_equal(got, want), lengths
+        assert np.array_equal(got_last, fresh.last()), lengths
+        fresh.free()
+    with pytest.raises(qattn.QattnError):
+        run.update(np.array([0, 5, 3], np.int32))  # decreasing offsets
+    run.update(cu_of([500] * 4))  # still usable
+    run.destroy()
+    for b in (bq, bk, bv, bo, bl):
+        b.free()
+
+
 def test_metric_size_1x5000_sparse_sampled(ctx, qattn, oracle):
     rows = np.unique(np.concatenate([np.arange(0, 5000, 23), [0, 175, 176, 431, 432, 607, 608, 609,
                                                              4990, 4999]]))
