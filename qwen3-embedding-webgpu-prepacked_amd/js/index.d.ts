@@ -65,6 +65,8 @@ export class CausalAttentionKernel {
             valueOffset?: number, options?: VarlenOptions): AttentionRun;
   createVarlenRun(q: DeviceBuffer, k: DeviceBuffer, v: DeviceBuffer, output: DeviceBuffer,
                   cuSeqlens: ArrayLike<number>, options?: VarlenOptions): AttentionRun;
+  /** Re-plans a run for the next batch of the same tensors (same options, new lengths). */
+  updateRun(run: AttentionRun, cuSeqlens: ArrayLike<number>): void;
   encode(run: AttentionRun): void;
   destroyRun(run: AttentionRun): void;
 }
@@ -75,10 +77,15 @@ export interface HipRuntimeOptions {
   /** Default true: embeddings are bitwise independent of batching (no split-K). */
   batchInvariant?: boolean;
 }
+export interface HipAttentionPlan extends EmbeddingPlan {
+  /** Host enqueue time and wall time (ms) of the last run, and its token count. */
+  readonly timing: { hostMs: number; totalMs: number; tokens: number } | null;
+  destroy(): void;
+}
 export class HipAttentionRuntime implements EmbeddingRuntime {
   constructor(options?: HipRuntimeOptions);
   readonly packing: 'varlen';
-  createPlan(batch: number, sequence: number): EmbeddingPlan;
+  createPlan(batch: number, sequence: number): HipAttentionPlan;
   destroy(): void;
 }
 
@@ -102,7 +109,14 @@ export interface PrepackedModel {
   buffer: ArrayBuffer;
   dataOffset: number;
 }
+/** Every rejection of the container code; `code` names the rule (e.g. 'BAD_MAGIC', 'TENSOR_OUT_OF_BOUNDS'). */
+export class PrepackedFormatError extends Error {
+  readonly code: 'NO_PARTS' | 'K_NOT_BLOCKS' | 'K_MISMATCH' | 'PART_SIZE' | 'TRUNCATED_PRELUDE' | 'BAD_MAGIC'
+    | 'TRUNCATED_HEADER' | 'BAD_LAYOUT' | 'TENSOR_OUT_OF_BOUNDS' | 'DUPLICATE_TENSOR' | 'BAD_COMPACT_TENSOR'
+    | 'BAD_STORAGE' | 'NO_TENSOR';
+}
 export const prepacked: {
+  PrepackedFormatError: typeof PrepackedFormatError;
   MAGIC: 'WGPACK02'; LAYOUT: 'q4_0-tile32-compact-v2'; TILE_ROWS: 32; BLOCK_VALUES: 32; BLOCK_BYTES: 20;
   STORAGE_COMPACT: 'q4_0-tile32-compact'; STORAGE_RAW: 'raw'; GGML_TYPE: { F32: 0; F16: 1; Q4_0: 2 };
   packQ40Tile32(name: string, parts: ReadonlyArray<{ name: string; k: number; n: number; bytes: Uint8Array }>): PackedTensorBytes;

@@ -62,19 +62,22 @@ test('tile order over several tiles and K blocks', () => {
   assert.ok(packed.bytes.slice(pad, pad + 20).every((b) => b === 0));
 });
 
+// The reference rejects these inputs (src/prepacked/format.ts); each rejection here is a
+// PrepackedFormatError naming the rule that failed.
 test('packing and parsing reject what the reference rejects', () => {
-  assert.throws(() => fmt.packQ40Tile32('x', []), /without tensor parts/);
-  assert.throws(() => fmt.packQ40Tile32('x', [{ name: 'a', k: 48, n: 1, bytes: new Uint8Array(27) }]), /not divisible by 32/);
+  const code = (c) => (e) => e instanceof fmt.PrepackedFormatError && e.code === c;
+  assert.throws(() => fmt.packQ40Tile32('x', []), code('NO_PARTS'));
+  assert.throws(() => fmt.packQ40Tile32('x', [{ name: 'a', k: 48, n: 1, bytes: new Uint8Array(27) }]), code('K_NOT_BLOCKS'));
   assert.throws(() => fmt.packQ40Tile32('x', [{ name: 'a', k: 32, n: 1, bytes: new Uint8Array(18) },
-    { name: 'b', k: 64, n: 1, bytes: new Uint8Array(36) }]), /mismatched K/);
-  assert.throws(() => fmt.packQ40Tile32('x', [{ name: 'a', k: 32, n: 2, bytes: new Uint8Array(18) }]), /expected 36/);
+    { name: 'b', k: 64, n: 1, bytes: new Uint8Array(36) }]), code('K_MISMATCH'));
+  assert.throws(() => fmt.packQ40Tile32('x', [{ name: 'a', k: 32, n: 2, bytes: new Uint8Array(18) }]), code('PART_SIZE'));
   const good = fmt.buildPrepackedFile('s', 1, {}, [fmt.rawTensor('t', [4], 0, new Uint8Array(16))]);
-  assert.throws(() => fmt.parsePrepackedModel(new ArrayBuffer(4)), /shorter than its prelude/);
+  assert.throws(() => fmt.parsePrepackedModel(new ArrayBuffer(4)), code('TRUNCATED_PRELUDE'));
   const badMagic = good.slice(); badMagic[0] = 0x58;
-  assert.throws(() => fmt.parsePrepackedModel(badMagic.buffer), /invalid prepacked model magic/);
+  assert.throws(() => fmt.parsePrepackedModel(badMagic.buffer), code('BAD_MAGIC'));
   const longHeader = good.slice(); new DataView(longHeader.buffer).setUint32(8, 1 << 30, true);
-  assert.throws(() => fmt.parsePrepackedModel(longHeader.buffer), /header extends past end/);
-  assert.throws(() => fmt.parsePrepackedModel(good.slice(0, good.byteLength - 1).buffer), /extends past end of prepacked file/);
+  assert.throws(() => fmt.parsePrepackedModel(longHeader.buffer), code('TRUNCATED_HEADER'));
+  assert.throws(() => fmt.parsePrepackedModel(good.slice(0, good.byteLength - 1).buffer), code('TENSOR_OUT_OF_BOUNDS'));
   const rebuild = (mutate) => {
     const p = fmt.parsePrepackedModel(good.slice().buffer);
     const header = JSON.parse(JSON.stringify(p.header));
@@ -87,10 +90,33 @@ test('packing and parsing reject what the reference rejects', () => {
     out.set(json, 12);
     return out.buffer;
   };
-  assert.throws(() => fmt.parsePrepackedModel(rebuild((h) => { h.layout = 'other'; })), /unsupported prepacked layout/);
-  assert.throws(() => fmt.parsePrepackedModel(rebuild((h) => { h.tensors.push(Object.assign({}, h.tensors[0])); })), /duplicate prepacked tensor/);
-  assert.throws(() => fmt.parsePrepackedModel(rebuild((h) => { h.tensors[0].storage = 'q4_0-tile32-compact'; })), /invalid compact Q4_0 metadata/);
-  assert.throws(() => fmt.parsePrepackedModel(rebuild((h) => { h.tensors[0].storage = 'zip'; })), /unsupported storage/);
+  for (const field of ['version', 'layout', 'tileRows', 'blockValues', 'blockBytes']) {
+    assert.throws(() => fmt.parsePrepackedModel(rebuild((h) => { h[field] = 'other'; })), code('BAD_LAYOUT'), field);
+  }
+  assert.throws(() => fmt.parsePrepackedModel(rebuild((h) => { h.tensors.push(Object.assign({}, h.tensors[0])); })), code('DUPLICATE_TENSOR'));
+  assert.throws(() => fmt.parsePrepackedModel(rebuild((h) => { h.tensors[0].storage = 'q4_0-tile32-compact'; })), code('BAD_COMPACT_TENSOR'));
+  assert.throws(() => fmt.parsePrepackedModel(rebuild((h) => { h.tensors[0].storage = 'zip'; })), code('BAD_STORAGE'));
+  // what it accepts: a compact 2-D Q4_0 entry, and an unchanged header
+  fmt.parsePrepackedModel(rebuild((h) => { Object.assign(h.tensors[0], { storage: 'q4_0-tile32-compact', type: 2, dimensions: [32, 1] }); }));
+  fmt.parsePrepackedModel(rebuild(() => {}));
+});
+
+test('the file layout: prelude, header length, aligned data start and tensor offsets', () => {
+  const a = fmt.rawTensor('a', [3], 0, new Uint8Array([1, 2, 3]));
+  const b = fmt.rawTensor('b', [300], 0, new Uint8Array(300).fill(7));
+  const c = fmt.rawTensor('c', [1], 0, new Uint8Array([9]));
+  const file = fmt.buildPrepackedFile('sha', 5, { k: 'v' }, [a, b, c]);
+  assert.strictEqual(Buffer.from(file.subarray(0, 8)).toString('latin1'), 'WGPACK02');
+  const n = new DataView(file.buffer).getUint32(8, true);
+  const header = JSON.parse(Buffer.from(file.subarray(12, 12 + n)).toString('utf8'));
+  assert.deepStrictEqual(header.tensors.map((t) => [t.offset, t.byteLength]), [[0, 3], [256, 300], [768, 1]]);
+  const start = Math.ceil((12 + n) / 256) * 256;
+  assert.strictEqual(file.byteLength, start + 769);
+  assert.deepStrictEqual(Array.from(file.subarray(start, start + 3)), [1, 2, 3]);
+  assert.strictEqual(file[start + 768], 9);
+  const parsed = fmt.parsePrepackedModel(file.buffer);
+  assert.strictEqual(parsed.dataOffset, start);
+  assert.strictEqual(parsed.tensors.get('b').byteOffset, start + 256);
 });
 
 (async () => {
