@@ -39,7 +39,8 @@
 extern "C" {
 #endif
 
-#define QATTN_ABI_VERSION 3
+/* 4: qattn_qk_norm_rope_qkv, qattn_run_update; qattn_qk_norm_rope takes heads in multiples of 4 */
+#define QATTN_ABI_VERSION 4
 
 #define QATTN_Q_HEADS 16
 #define QATTN_KV_HEADS 8
