@@ -18,6 +18,12 @@
  *   last-token row of poolShader       ops.ts:357       | qattn_run_desc.o_last
  *   LastTokenPoolKernel (L2 norm)      ops.ts:347-379   | qattn_pool_last_l2
  *   compact Q4_0 batch matmul   quant-matmul.ts:267-307 | qattn_q4_matmul
+ *   EmbeddingLookupKernel (Q6_K)       ops.ts:381-423   | qattn_embed_q6k
+ *   RmsNormKernel (residual + norm)    ops.ts:21-72     | qattn_rmsnorm
+ *   SwiGLUKernel                       ops.ts:74-102    | qattn_swiglu
+ *   Qwen3WebGPUModel (weights)         model.ts:185-255 | qattn_model_create / _destroy
+ *   Qwen3ExecutionPlan (28 layers)     model.ts:49-139  | qattn_model_plan_create / _run / _destroy
+ *   Qwen3ExecutionPlan.profile()       model.ts:141-182 | qattn_model_plan_profile
  *
  * Fixed model geometry (model.ts:18-23, ops.ts:196): 16 query heads, 8 KV heads (query head h
  * reads KV head h/2), head_dim 128, scale 1/sqrt(128), fp16 storage, fp32 accumulation.
@@ -39,8 +45,10 @@
 extern "C" {
 #endif
 
-/* 4: qattn_qk_norm_rope_qkv, qattn_run_update; qattn_qk_norm_rope takes heads in multiples of 4 */
-#define QATTN_ABI_VERSION 4
+/* 4: qattn_qk_norm_rope_qkv, qattn_run_update; qattn_qk_norm_rope takes heads in multiples of 4
+ * 5: the model forward: qattn_embed_q6k, qattn_rmsnorm, qattn_swiglu, qattn_model_*,
+ *    qattn_model_plan_* */
+#define QATTN_ABI_VERSION 5
 
 #define QATTN_Q_HEADS 16
 #define QATTN_KV_HEADS 8
@@ -263,6 +271,117 @@ int qattn_q4_matmul(qattn_ctx* ctx, const void* x, int64_t ldx, int32_t M, int32
 int qattn_pool_last_l2(qattn_ctx* ctx, const void* x, int64_t row_stride, int32_t width,
                        const int32_t* cu_seqlens, int32_t nseq, float* out, int64_t out_row_stride,
                        qattn_stream_t stream);
+
+/* ---- the model forward around the attention path  (model.ts:18-23, 49-183) ----------------- */
+#define QATTN_HIDDEN 1024       /* model.ts:18 */
+#define QATTN_INTERMEDIATE 3072 /* model.ts:19 */
+#define QATTN_MAX_LAYERS 28     /* model.ts:21 */
+#define QATTN_Q6K_BLOCK_BYTES 210
+
+/* out[t*out_row_stride + c] = row ids[t] of a Q6_K table, dequantised as the reference's
+ * embedding shader does (ops.ts:381-412): value i = 128h + 32quad + l of a 256-value block is
+ * f16(f32(d) * f32(scale[8h + l/16 + 2quad]) * f32(q - 32)), q the 6-bit code of ql / qh.  `ids`:
+ * device int32 [tokens]; ids outside [0, vocab) give zero rows (the model plan rejects them on the
+ * host first).  `table`: device, width/256 blocks of 210 bytes per row, vocab = table_bytes /
+ * (width/256 * 210) rows; width a multiple of 256; out 16-byte aligned, out_row_stride a multiple
+ * of 8 and >= width.  Enqueued on `stream`; allocates nothing. */
+int qattn_embed_q6k(qattn_ctx* ctx, const int32_t* ids, int64_t tokens, const void* table,
+                    int64_t table_bytes, int32_t width, void* out, int64_t out_row_stride,
+                    qattn_stream_t stream);
+/* Residual add + RMSNorm of `rows` fp16 rows of `width` (ops.ts:21-57): with a residual,
+ * v = f32(x) + f32(residual) and x <- f16(v) in place; without, v = f32(x).  Then
+ * out = f16(f32(x) * inv * weight[c]) with inv = 1/sqrt(sum(v^2)/width + eps), the sum over the
+ * unrounded v as in the reference.  weight: device f32 [width]; residual may be NULL; out may
+ * not alias x.  width a multiple of 8, <= 4096; pointers 16-byte aligned; strides multiples of 8
+ * elements.  Enqueued on `stream`; allocates nothing. */
+int qattn_rmsnorm(qattn_ctx* ctx, void* x, int64_t x_row_stride, const void* residual,
+                  int64_t residual_row_stride, const float* weight, void* out,
+                  int64_t out_row_stride, int64_t rows, int32_t width, double eps,
+                  qattn_stream_t stream);
+/* out[r][c] = f16(silu(g) * u), g = gate_up[r][c], u = gate_up[r][width + c], silu(g) =
+ * g / (1 + exp(-g)) in f32 (ops.ts:74-89).  width a multiple of 8; gate_up_row_stride >=
+ * 2*width, out_row_stride >= width, multiples of 8; pointers 16-byte aligned.  Enqueued on
+ * `stream`; allocates nothing. */
+int qattn_swiglu(qattn_ctx* ctx, const void* gate_up, int64_t gate_up_row_stride, void* out,
+                 int64_t out_row_stride, int64_t rows, int32_t width, qattn_stream_t stream);
+
+/* Device weights of one transformer layer (tensor names of the reference's prepacked file,
+ * model.ts:86-106; compact tensors in the q4_0-tile32-compact layout of qattn_q4_matmul, norm
+ * gains f32).  The library reads them in place and never frees them. */
+typedef struct qattn_layer_weights {
+  const float* attn_norm;   /* blk.N.attn_norm.weight    [1024] */
+  const void* attn_qkv;     /* blk.N.attn_qkv.weight     1024 -> 4096 (Q 2048 | K 1024 | V 1024) */
+  int64_t attn_qkv_bytes;
+  const float* attn_q_norm; /* blk.N.attn_q_norm.weight  [128] */
+  const float* attn_k_norm; /* blk.N.attn_k_norm.weight  [128] */
+  const void* attn_output;  /* blk.N.attn_output.weight  2048 -> 1024 */
+  int64_t attn_output_bytes;
+  const float* ffn_norm;    /* blk.N.ffn_norm.weight     [1024] */
+  const void* ffn_gate_up;  /* blk.N.ffn_gate_up.weight  1024 -> 6144 (gate 3072 | up 3072) */
+  int64_t ffn_gate_up_bytes;
+  const void* ffn_down;     /* blk.N.ffn_down.weight     3072 -> 1024 */
+  int64_t ffn_down_bytes;
+} qattn_layer_weights;
+
+typedef struct qattn_model_desc {
+  const void* token_embd;   /* token_embd.weight: Q6_K [vocab][1024] (4 blocks of 210 B per row) */
+  int64_t token_embd_bytes;
+  const float* output_norm; /* output_norm.weight [1024] */
+  int32_t n_layers;         /* 1 .. QATTN_MAX_LAYERS (the model has 28) */
+  const qattn_layer_weights* layers; /* host array of n_layers; copied */
+  double eps;               /* RMSNorm epsilon (model.ts:22: 1e-6) */
+  double rope_theta;        /* model.ts:23: 1e6 */
+  int32_t mask;             /* attention mask (enum qattn_mask_kind; the model uses PREFIX_LOCAL) */
+  int32_t prefix, window;   /* 176, 432 (ops.ts:206) */
+} qattn_model_desc;
+
+typedef struct qattn_model qattn_model;
+typedef struct qattn_model_plan qattn_model_plan;
+
+/* Checks and keeps the weight pointers (no copies of the tensors). */
+int qattn_model_create(qattn_ctx* ctx, const qattn_model_desc* desc, qattn_model** out);
+void qattn_model_destroy(qattn_model* model);
+
+/* An execution plan for up to max_tokens packed tokens in up to max_seqs sequences: owns the
+ * activations (residual stream, normalised rows, qkvRaw, q, k, attention output, FFN buffers --
+ * model.ts:62-75) and one attention run, re-planned per batch.  The model must outlive it. */
+int qattn_model_plan_create(qattn_model* model, int32_t max_tokens, int32_t max_seqs,
+                            qattn_model_plan** out);
+void qattn_model_plan_destroy(qattn_model_plan* plan);
+
+/* One batch (Qwen3ExecutionPlan.run, model.ts:113-139, over a packed varlen batch): host token
+ * ids [cu_seqlens[nseq]] (each in [0, vocab)) and host cu_seqlens (nseq+1 offsets, as in
+ * qattn_run_desc).  Embedding lookup and the initial norm, then per layer: QKV projection,
+ * QK-norm + RoPE (positions restart at 0 per sequence), attention, output projection, residual +
+ * norm, gate/up projection, SwiGLU, down projection, residual + next norm (the next layer's
+ * attn_norm, output_norm after the last); then the last-token pool + L2 normalisation into
+ * out[i*out_row_stride + c], f32, c < 1024, a device pointer (16-byte aligned, stride a multiple
+ * of 4).  The ids are copied to the device before the call returns; the rest is enqueued on
+ * `stream` (the plan's buffers are reused by the next call, which must come after this one on the
+ * same stream or after a synchronisation). */
+int qattn_model_plan_run(qattn_model_plan* plan, const int32_t* ids, const int32_t* cu_seqlens,
+                         int32_t nseq, float* out, int64_t out_row_stride, qattn_stream_t stream);
+
+/* The stages of one run, as the reference's profile() names them (model.ts:157-168). */
+enum qattn_model_stage {
+  QATTN_STAGE_EMBEDDING_NORM = 0,
+  QATTN_STAGE_QKV = 1,
+  QATTN_STAGE_ROPE_ATTENTION = 2,
+  QATTN_STAGE_ATTENTION_OUTPUT = 3,
+  QATTN_STAGE_POST_ATTENTION_NORM = 4,
+  QATTN_STAGE_FFN_UP_GATE = 5,
+  QATTN_STAGE_SWIGLU = 6,
+  QATTN_STAGE_FFN_DOWN = 7,
+  QATTN_STAGE_POST_FFN_NORM = 8,
+  QATTN_STAGE_POOL = 9,
+  QATTN_STAGE_COUNT = 10
+};
+/* qattn_model_plan_run with a HIP event pair around every stage of every layer, then a wait for
+ * the stream: stage_ms[s] receives stage s's total over all layers in milliseconds
+ * (Qwen3ExecutionPlan.profile, model.ts:141-182). */
+int qattn_model_plan_profile(qattn_model_plan* plan, const int32_t* ids, const int32_t* cu_seqlens,
+                             int32_t nseq, float* out, int64_t out_row_stride, qattn_stream_t stream,
+                             float stage_ms[QATTN_STAGE_COUNT]);
 
 /* ---- synthetic inputs ---------------------------------------------------------------------- */
 /* Element (r, c), r < rows, c < row_elems, at dst[r*row_stride + c] receives

@@ -17,6 +17,7 @@
 
 #include "../../include/qattn.h"
 #include "attn_common.h"
+#include "context.h"
 #include "planner.h"
 #include "qk_rope.h"
 
@@ -49,20 +50,6 @@ constexpr size_t kScratchBytes = (size_t)1 << 20;
 }
 static __device__ __align__(256) char scratch[kScratchBytes];
 
-struct qattn_ctx {
-  int device = 0;
-  int cu_count = 0;
-  hipStream_t stream = nullptr;
-  void* scratch = nullptr;  // this device's copy of `scratch` (qattn_prefill_static)
-  // RoPE table of the producer, [positions][64] (cos, sin), built for `rope_theta`; grown when a
-  // longer sequence arrives (the reference builds one per plan, model.ts:76-83).
-  float2* rope = nullptr;
-  int32_t rope_positions = 0;
-  double rope_theta = 0.0;
-  std::string last_error;
-  std::mutex mu;
-};
-
 struct qattn_run {
   qattn_ctx* ctx = nullptr;
   AttnParams params{};
@@ -76,47 +63,28 @@ struct qattn_run {
 };
 
 namespace {
-
 thread_local std::string g_last_error;
+}  // namespace
 
-int fail(qattn_ctx* ctx, int code, const char* fmt, ...) __attribute__((format(printf, 3, 4)));
+namespace qattn {
+
 int fail(qattn_ctx* ctx, int code, const char* fmt, ...) {
   char buf[512];
   va_list ap;
   va_start(ap, fmt);
   vsnprintf(buf, sizeof(buf), fmt, ap);
   va_end(ap);
-  g_last_error = buf;
-  if (ctx) {
-    std::lock_guard<std::mutex> lock(ctx->mu);
-    ctx->last_error = buf;
-  }
+  set_last_error(ctx, buf);
   return code;
 }
 
-#define HIP_TRY(ctx, expr)                                                                   \
-  do {                                                                                       \
-    hipError_t e_ = (expr);                                                                  \
-    if (e_ != hipSuccess)                                                                    \
-      return fail((ctx), QATTN_EHIP, "%s failed: %s", #expr, hipGetErrorString(e_));        \
-  } while (0)
-
-struct DeviceGuard {
-  int prev = -1;
-  explicit DeviceGuard(int dev) {
-    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
-    if (prev != dev) (void)hipSetDevice(dev);
+void set_last_error(qattn_ctx* ctx, const std::string& message) {
+  g_last_error = message;
+  if (ctx) {
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    ctx->last_error = message;
   }
-  ~DeviceGuard() {
-    if (prev >= 0) (void)hipSetDevice(prev);
-  }
-};
-
-hipStream_t pick_stream(qattn_ctx* ctx, qattn_stream_t s) {
-  return s ? reinterpret_cast<hipStream_t>(s) : ctx->stream;
 }
-
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 int validate_cu(qattn_ctx* ctx, const int32_t* cu, int32_t nseq) {
   if (!cu) return fail(ctx, QATTN_EINVAL, "cu_seqlens is NULL");
@@ -129,6 +97,10 @@ int validate_cu(qattn_ctx* ctx, const int32_t* cu, int32_t nseq) {
                   cu[i + 1]);
   return QATTN_OK;
 }
+
+}  // namespace qattn
+
+namespace {
 
 int validate_desc(qattn_ctx* ctx, const qattn_run_desc* d) {
   if (!d) return fail(ctx, QATTN_EINVAL, "desc is NULL");

@@ -1,0 +1,25 @@
+// model_ops.h -- launchers of the row-wise model kernels (model_ops.hip) and their limits.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "attn_common.h"
+
+namespace qattn {
+
+constexpr int kQ6KBlockBytes = 210;   // GGML Q6_K: 256 values (ggml block_q6_K)
+constexpr int kRmsMaxWidth = 4096;    // rmsnorm_kernel: columns per row (one wavefront, 8 per lane per pass)
+
+// out[t][c] (c < width, a multiple of 256) = token ids[t]'s row of the Q6_K table of `vocab` rows;
+// ids outside [0, vocab) give zero rows.
+hipError_t launch_embed_q6k(const int32_t* ids, int64_t tokens, const uint8_t* table, int64_t vocab, int width,
+                            half_t* out, int64_t out_stride, hipStream_t stream);
+// Residual add (residual may be NULL) + RMSNorm of `rows` rows of `width` (multiple of 8, <= kRmsMaxWidth).
+hipError_t launch_rmsnorm(half_t* x, const half_t* residual, const float* weight, half_t* out, int64_t rows,
+                          int width, int64_t x_stride, int64_t r_stride, int64_t out_stride, float eps,
+                          hipStream_t stream);
+// out = silu(gate) * up for rows of [gate (width) | up (width)], width a multiple of 8.
+hipError_t launch_swiglu(const half_t* gate_up, int64_t gu_stride, half_t* out, int64_t out_stride, int64_t rows,
+                         int width, hipStream_t stream);
+
+}  // namespace qattn

@@ -54,6 +54,37 @@ class RunInfo(ctypes.Structure):
         return {name: getattr(self, name) for name, _ in self._fields_}
 
 
+HIDDEN, INTERMEDIATE, MAX_LAYERS, Q6K_BLOCK_BYTES = 1024, 3072, 28, 210
+# enum qattn_model_stage, in the reference's profile() order (model.ts:157-168)
+STAGES = ("embedding_norm", "qkv", "rope_attention", "attention_output", "post_attention_norm",
+          "ffn_up_gate", "swiglu", "ffn_down", "post_ffn_norm", "pool")
+
+
+class LayerWeights(ctypes.Structure):
+    """qattn_layer_weights: device pointers of one layer's tensors (model.ts:86-106)."""
+    _fields_ = [
+        ("attn_norm", ctypes.c_void_p),
+        ("attn_qkv", ctypes.c_void_p), ("attn_qkv_bytes", ctypes.c_int64),
+        ("attn_q_norm", ctypes.c_void_p), ("attn_k_norm", ctypes.c_void_p),
+        ("attn_output", ctypes.c_void_p), ("attn_output_bytes", ctypes.c_int64),
+        ("ffn_norm", ctypes.c_void_p),
+        ("ffn_gate_up", ctypes.c_void_p), ("ffn_gate_up_bytes", ctypes.c_int64),
+        ("ffn_down", ctypes.c_void_p), ("ffn_down_bytes", ctypes.c_int64),
+    ]
+
+
+class ModelDesc(ctypes.Structure):
+    """qattn_model_desc."""
+    _fields_ = [
+        ("token_embd", ctypes.c_void_p), ("token_embd_bytes", ctypes.c_int64),
+        ("output_norm", ctypes.c_void_p),
+        ("n_layers", ctypes.c_int32),
+        ("layers", ctypes.POINTER(LayerWeights)),
+        ("eps", ctypes.c_double), ("rope_theta", ctypes.c_double),
+        ("mask", ctypes.c_int32), ("prefix", ctypes.c_int32), ("window", ctypes.c_int32),
+    ]
+
+
 def build():
     """Compile libqattn.so for gfx950 with the package Makefile."""
     subprocess.run(["make", "-s", "-C", PKG_DIR, "lib"], check=True)
@@ -114,6 +145,15 @@ def lib():
         "qattn_event_record": (ctypes.c_int, [vp, vp]),
         "qattn_event_elapsed_ms": (ctypes.c_int, [vp, vp, ctypes.POINTER(ctypes.c_float)]),
         "qattn_event_destroy": (ctypes.c_int, [vp]),
+        "qattn_embed_q6k": (ctypes.c_int, [vp, vp, i64, vp, i64, i32, vp, i64, vp]),
+        "qattn_rmsnorm": (ctypes.c_int, [vp, vp, i64, vp, i64, vp, vp, i64, i64, i32, ctypes.c_double, vp]),
+        "qattn_swiglu": (ctypes.c_int, [vp, vp, i64, vp, i64, i64, i32, vp]),
+        "qattn_model_create": (ctypes.c_int, [vp, ctypes.POINTER(ModelDesc), pvp]),
+        "qattn_model_destroy": (None, [vp]),
+        "qattn_model_plan_create": (ctypes.c_int, [vp, i32, i32, pvp]),
+        "qattn_model_plan_destroy": (None, [vp]),
+        "qattn_model_plan_run": (ctypes.c_int, [vp, vp, vp, i32, vp, i64, vp]),
+        "qattn_model_plan_profile": (ctypes.c_int, [vp, vp, vp, i32, vp, i64, vp, vp]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -375,6 +415,94 @@ class Context:
 
     def event(self):
         return Event(self)
+
+    def embed_q6k(self, ids_ptr, tokens, table_ptr, table_bytes, out_ptr, width=HIDDEN, out_row_stride=None,
+                  stream=None):
+        """Q6_K token-embedding rows (EmbeddingLookupKernel, ops.ts:381-423)."""
+        _check(lib().qattn_embed_q6k(self.handle, ids_ptr, tokens, table_ptr, table_bytes, width, out_ptr,
+                                     width if out_row_stride is None else out_row_stride, stream), self.handle)
+
+    def rmsnorm(self, x_ptr, weight_ptr, out_ptr, rows, width=HIDDEN, residual_ptr=None, eps=1e-6,
+                x_row_stride=None, residual_row_stride=None, out_row_stride=None, stream=None):
+        """Residual add (in place on x) + RMSNorm (RmsNormKernel, ops.ts:21-72)."""
+        _check(lib().qattn_rmsnorm(self.handle, x_ptr, width if x_row_stride is None else x_row_stride,
+                                   residual_ptr, width if residual_row_stride is None else residual_row_stride,
+                                   weight_ptr, out_ptr, width if out_row_stride is None else out_row_stride,
+                                   rows, width, eps, stream), self.handle)
+
+    def swiglu(self, gate_up_ptr, out_ptr, rows, width=INTERMEDIATE, gate_up_row_stride=None,
+               out_row_stride=None, stream=None):
+        """silu(gate) * up (SwiGLUKernel, ops.ts:74-102)."""
+        _check(lib().qattn_swiglu(self.handle, gate_up_ptr,
+                                  2 * width if gate_up_row_stride is None else gate_up_row_stride, out_ptr,
+                                  width if out_row_stride is None else out_row_stride, rows, width, stream),
+               self.handle)
+
+    def model(self, token_embd, output_norm, layers, eps=1e-6, rope_theta=1e6, mask=MASK_PREFIX_LOCAL,
+              prefix=176, window=432):
+        """qattn_model_create over device tensors: token_embd = (ptr, bytes), output_norm = ptr,
+        layers = list of dicts with the LayerWeights field names (compact tensors as (ptr, bytes))."""
+        return Model(self, token_embd, output_norm, layers, eps, rope_theta, mask, prefix, window)
+
+
+class Model:
+    """The weights of the forward (Qwen3WebGPUModel, model.ts:185-255); plan() makes an
+    execution plan (Qwen3ExecutionPlan, model.ts:49-183)."""
+
+    def __init__(self, ctx, token_embd, output_norm, layers, eps, rope_theta, mask, prefix, window):
+        self.ctx = ctx
+        arr = (LayerWeights * len(layers))()
+        for i, lw in enumerate(layers):
+            for name in ("attn_norm", "attn_q_norm", "attn_k_norm", "ffn_norm"):
+                setattr(arr[i], name, lw[name])
+            for name in ("attn_qkv", "attn_output", "ffn_gate_up", "ffn_down"):
+                ptr, nbytes = lw[name]
+                setattr(arr[i], name, ptr)
+                setattr(arr[i], name + "_bytes", nbytes)
+        d = ModelDesc(token_embd[0], token_embd[1], output_norm, len(layers),
+                      ctypes.cast(arr, ctypes.POINTER(LayerWeights)), eps, rope_theta, mask, prefix, window)
+        h = ctypes.c_void_p()
+        _check(lib().qattn_model_create(ctx.handle, ctypes.byref(d), ctypes.byref(h)), ctx.handle)
+        self.handle = h
+
+    def plan(self, max_tokens, max_seqs=16):
+        return ModelPlan(self, max_tokens, max_seqs)
+
+    def destroy(self):
+        if self.handle:
+            lib().qattn_model_destroy(self.handle)
+            self.handle = None
+
+
+class ModelPlan:
+    def __init__(self, model, max_tokens, max_seqs):
+        self.model = model
+        h = ctypes.c_void_p()
+        _check(lib().qattn_model_plan_create(model.handle, max_tokens, max_seqs, ctypes.byref(h)),
+               model.ctx.handle)
+        self.handle = h
+
+    def run(self, ids, cu_seqlens, out_ptr, out_row_stride=HIDDEN, stream=None):
+        """Enqueue one packed batch; out_ptr: device f32 [nseq, out_row_stride]."""
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        cu = np.ascontiguousarray(cu_seqlens, dtype=np.int32)
+        _check(lib().qattn_model_plan_run(self.handle, _np_ptr(ids) if ids.size else None, _np_ptr(cu),
+                                          len(cu) - 1, out_ptr, out_row_stride, stream), self.model.ctx.handle)
+
+    def profile(self, ids, cu_seqlens, out_ptr, out_row_stride=HIDDEN, stream=None):
+        """One batch with per-stage timing: {stage name: ms over all layers}."""
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        cu = np.ascontiguousarray(cu_seqlens, dtype=np.int32)
+        ms = np.zeros(len(STAGES), dtype=np.float32)
+        _check(lib().qattn_model_plan_profile(self.handle, _np_ptr(ids) if ids.size else None, _np_ptr(cu),
+                                              len(cu) - 1, out_ptr, out_row_stride, stream, _np_ptr(ms)),
+               self.model.ctx.handle)
+        return dict(zip(STAGES, (float(x) for x in ms)))
+
+    def destroy(self):
+        if self.handle:
+            lib().qattn_model_plan_destroy(self.handle)
+            self.handle = None
 
 
 def header_symbols(path=HEADER_PATH):
