@@ -373,6 +373,103 @@ def q4_timing(reps):
     ctx.close()
 
 
+def synthetic_model(ctx, q, n_layers, vocab, seed=0, scale=0.005):
+    """Random weights of the model's shapes, written straight into the device layouts the forward
+    reads (no file, no packing step): a Q6_K token table of `vocab` rows (random codes, int8
+    scales 1..15 with random sign, d ~ 0.006), norm gains 1 + 0.1 N(0,1), and per layer the four
+    q4_0-tile32-compact projections as random 20-byte records (f16 scale ~ `scale`, two zero
+    bytes, nibbles 1..15 so the weights q - 8 are zero-mean).  Returns (model, buffers)."""
+    rng = np.random.default_rng(seed)
+    bufs = []
+
+    def up(a):
+        b = ctx.upload(np.ascontiguousarray(a))
+        bufs.append(b)
+        return b
+
+    def compact(K, N):
+        nbytes = q.lib().qattn_q4_compact_bytes(K, N)
+        rec = np.empty((nbytes // 20, 20), np.uint8)
+        rec[:, 0:2] = (scale * rng.uniform(0.5, 1.5, (len(rec), 1))).astype(np.float16).view(np.uint8)
+        rec[:, 2:4] = 0
+        rec[:, 4:] = (rng.integers(1, 16, (len(rec), 16)) | rng.integers(1, 16, (len(rec), 16)) << 4).astype(np.uint8)
+        return (up(rec).ptr, nbytes)
+
+    gain = lambda n: up((1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)).ptr
+    blocks = rng.integers(0, 256, (vocab, 4, 210), dtype=np.uint8)
+    blocks[..., 192:208] = (rng.integers(1, 16, (vocab, 4, 16)) * rng.choice([-1, 1], (vocab, 4, 16))).astype(np.int8).view(np.uint8)
+    blocks[..., 208:210] = (0.006 * rng.uniform(0.5, 1.5, (vocab, 4, 1))).astype(np.float16).view(np.uint8)
+    table = up(blocks)
+    layers = [{"attn_norm": gain(1024), "attn_qkv": compact(1024, 4096), "attn_q_norm": gain(128),
+               "attn_k_norm": gain(128), "attn_output": compact(2048, 1024), "ffn_norm": gain(1024),
+               "ffn_gate_up": compact(1024, 6144), "ffn_down": compact(3072, 1024)} for _ in range(n_layers)]
+    model = ctx.model((table.ptr, blocks.nbytes), gain(1024), layers)
+    return model, bufs
+
+
+MODEL_VOCAB = 151669  # Qwen3 tokenizer vocabulary (the reference's token_embd rows)
+
+
+def retained_pairs_sparse(L, prefix=176, window=432):
+    """Retained (q, k) pairs of one sequence under the model's prefix + local mask (ops.ts:206):
+    every key up to q while q < prefix + window, then exactly prefix + window keys per query."""
+    n = min(L, prefix + window)
+    return n * (n + 1) // 2 + max(0, L - prefix - window) * (prefix + window)
+
+
+def model_timing(reps):
+    """The whole 28-layer forward (f4; not the headline metric): qattn_model_plan_run -- embedding
+    lookup, 28 x (norms, four Q4_0 projections, QK-norm + RoPE, attention, SwiGLU), pool -- on
+    synthetic weights at the BASELINE packings, random token ids over the full vocabulary.
+    `reps` forwards between HIP events per config after 2 warm-up runs, then one profiled run for
+    the per-stage split (the reference's profile() stages, model.ts:157-168).  FLOP counts the
+    projections (2 x 15.73 M per token per layer) and the attention pairs."""
+    q = load_binding()
+    ctx = q.Context(0)
+    model, bufs = synthetic_model(ctx, q, LAYERS, MODEL_VOCAB)
+    rng = np.random.default_rng(1)
+    gemm_flop_per_token = 2.0 * (1024 * 4096 + 2048 * 1024 + 1024 * 6144 + 3072 * 1024) * LAYERS
+    for name in ("full", "sparse", "cfg4", "cfg1", "cfg3"):
+        lengths = lengths_of(name)
+        cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+        T = int(cu[-1])
+        mask_pairs = sum(retained_pairs_sparse(L) for L in lengths)
+        ids = rng.integers(0, MODEL_VOCAB, T).astype(np.int32)
+        plan = model.plan(T, len(lengths))
+        out = ctx.alloc(len(lengths) * 1024 * 4)
+        for _ in range(2):
+            plan.run(ids, cu, out.ptr)
+        e0, e1 = ctx.event(), ctx.event()
+        ctx.synchronize()
+        e0.record()
+        for _ in range(reps):
+            plan.run(ids, cu, out.ptr)
+        e1.record()
+        ctx.synchronize()
+        ms = e0.elapsed_ms(e1) / reps
+        stages = plan.profile(ids, cu, out.ptr)
+        emb = out.read(np.float32, (len(lengths), 1024))
+        flop = gemm_flop_per_token * T + 8192.0 * mask_pairs * LAYERS
+        print(json.dumps({"path": "qattn_model_plan_run (28 layers)", "workload": name, "sequences": len(lengths),
+                          "tokens": T, "runs": reps, "ms_per_forward": round(ms, 3),
+                          "tokens_per_s": round(T / (ms / 1e3), 1),
+                          "requests_per_s": round(len(lengths) / (ms / 1e3), 1),
+                          "TFLOP/s": round(flop / (ms / 1e3) / 1e12, 1),
+                          "frac_of_fp16_peak": round(flop / (ms / 1e3) / 1e12 / PEAK_FP16_TFLOPS, 3),
+                          "stage_ms": {k: round(v, 3) for k, v in stages.items()},
+                          "embeddings_finite": bool(np.isfinite(emb).all()),
+                          "embedding_norms": [round(float(x), 4) for x in np.linalg.norm(emb, axis=1)[:4]]}),
+              flush=True)
+        out.free()
+        plan.destroy()
+        e0.destroy()
+        e1.destroy()
+    model.destroy()
+    for b in bufs:
+        b.free()
+    ctx.close()
+
+
 def kernel_sources_sha():
     """Hash of the sources the attention launch is built from (kernels and planner): HBM traffic
     measured on other sources (profiles/traffic.json) is not reported as this build's."""
@@ -401,7 +498,12 @@ def main():
                     help="only time N launches of the Q4_0 dequant-GEMM per projection shape and exit")
     ap.add_argument("--rope", type=int, default=0, metavar="N",
                     help="only time N launches of the fused QK-norm + RoPE producer and exit")
+    ap.add_argument("--model", type=int, default=0, metavar="N",
+                    help="only time N runs of the whole 28-layer forward (synthetic weights) per config and exit")
     args = ap.parse_args()
+    if args.model:
+        model_timing(args.model)
+        return
     if args.rope:
         rope_timing(args.rope)
         return

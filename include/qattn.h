@@ -333,6 +333,9 @@ typedef struct qattn_model_desc {
   double rope_theta;        /* model.ts:23: 1e6 */
   int32_t mask;             /* attention mask (enum qattn_mask_kind; the model uses PREFIX_LOCAL) */
   int32_t prefix, window;   /* 176, 432 (ops.ts:206) */
+  int32_t flags;            /* the attention run's enum qattn_run_flags: QATTN_FLAG_BATCH_INVARIANT
+                             * makes a sequence's embedding bitwise independent of its batch (every
+                             * other stage is row-wise or per sequence already) */
 } qattn_model_desc;
 
 typedef struct qattn_model qattn_model;

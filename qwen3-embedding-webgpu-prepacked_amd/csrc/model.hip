@@ -128,6 +128,7 @@ int qattn_model_create(qattn_ctx* ctx, const qattn_model_desc* d, qattn_model** 
     return fail(ctx, QATTN_EINVAL, "unknown mask kind %d", d->mask);
   if (d->mask == QATTN_MASK_PREFIX_LOCAL && (d->prefix < 0 || d->window < 0 || (d->prefix == 0 && d->window == 0)))
     return fail(ctx, QATTN_EINVAL, "prefix %d / window %d: >= 0, not both 0", d->prefix, d->window);
+  if (d->flags & ~QATTN_FLAG_BATCH_INVARIANT) return fail(ctx, QATTN_EINVAL, "unknown flags 0x%x", d->flags);
   struct Gemm {
     const char* name;
     const void* w;
@@ -356,6 +357,7 @@ int qattn_model_plan_create(qattn_model* model, int32_t max_tokens, int32_t max_
   rd.mask = model->desc.mask;
   rd.prefix = model->desc.prefix;
   rd.window = model->desc.window;
+  rd.flags = model->desc.flags;
   int rc = qattn_run_create(ctx, &rd, &p->run);
   if (rc) {
     free_plan(p);

@@ -41,11 +41,15 @@ namespace {
 // before the context), and their handles then report "destroyed" instead of touching freed memory.
 struct Buf;
 struct Run;
+struct Model;
+struct Plan;
 struct Ctx {
   qattn_ctx* ctx = nullptr;
   int refs = 1;  // the context handle's own reference
   std::set<Buf*> bufs;
   std::set<Run*> runs;
+  std::set<Model*> models;
+  std::set<Plan*> plans;
 };
 struct Buf {
   Ctx* owner = nullptr;
@@ -62,6 +66,23 @@ struct Run {
   std::vector<const Buf*> bound;
   int64_t max_tokens = 0;
   int64_t max_seqs = 0;  // o_last rows (no limit without o_last)
+};
+
+// A model (qattn_model over uploaded weight buffers) holds a reference on each weight buffer; an
+// execution plan made from it points back at it.  Destroying or collecting a model first destroys
+// the device side of its plans (their handles then report "destroyed").
+struct Model {
+  Ctx* owner = nullptr;
+  qattn_model* model = nullptr;
+  std::vector<napi_ref> bound_refs;
+  std::set<Plan*> plans;
+};
+struct Plan {
+  Ctx* owner = nullptr;
+  Model* model = nullptr;
+  qattn_model_plan* plan = nullptr;
+  napi_ref model_ref = nullptr;  // keeps the model's handle alive while the plan is
+  int64_t max_tokens = 0, max_seqs = 0;
 };
 
 void release_device(Ctx* c);
@@ -137,6 +158,16 @@ bool typed_bytes(napi_env env, napi_value v, void** data, size_t* bytes) {
 // Runs, then buffers, then the device context: everything still alive on `c`.
 void release_device(Ctx* c) {
   if (!c->ctx) return;
+  for (Plan* p : c->plans)
+    if (p->plan) {
+      qattn_model_plan_destroy(p->plan);
+      p->plan = nullptr;
+    }
+  for (Model* m : c->models)
+    if (m->model) {
+      qattn_model_destroy(m->model);
+      m->model = nullptr;
+    }
   for (Run* r : c->runs)
     if (r->run) {
       qattn_run_destroy(r->run);
@@ -814,6 +845,250 @@ napi_value PoolLastL2(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
+// ---- the model forward (Qwen3WebGPUModel / Qwen3ExecutionPlan, model.ts:49-255) --------------
+
+void drop_model_plans(Model* m) {
+  for (Plan* p : m->plans) {
+    if (p->plan) qattn_model_plan_destroy(p->plan);
+    p->plan = nullptr;
+    p->model = nullptr;
+  }
+  m->plans.clear();
+}
+void finalize_model(napi_env env, void* data, void*) {
+  auto* m = static_cast<Model*>(data);
+  Ctx* c = m->owner;
+  if (c->ctx) {
+    drop_model_plans(m);
+    if (m->model) qattn_model_destroy(m->model);
+  }
+  for (napi_ref ref : m->bound_refs) napi_delete_reference(env, ref);
+  for (Plan* p : m->plans) p->model = nullptr;
+  c->models.erase(m);
+  delete m;
+  unref(c);
+}
+void finalize_plan(napi_env env, void* data, void*) {
+  auto* p = static_cast<Plan*>(data);
+  Ctx* c = p->owner;
+  if (p->plan && c->ctx) qattn_model_plan_destroy(p->plan);
+  if (p->model) p->model->plans.erase(p);
+  if (p->model_ref) napi_delete_reference(env, p->model_ref);
+  c->plans.erase(p);
+  delete p;
+  unref(c);
+}
+
+// createModel(ctx, {tokenEmbd, outputNorm, layers: [{attnNorm, attnQkv, attnQNorm, attnKNorm,
+// attnOutput, ffnNorm, ffnGateUp, ffnDown}], eps, ropeTheta, mask, prefix, window, batchInvariant})
+// -> external.  Every tensor is a device buffer of this context holding exactly that tensor's
+// bytes (a compact projection's size is its buffer's); norm gains must hold their width of f32.
+napi_value CreateModel(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!args_of(env, info, 2, argv)) return nullptr;
+  Ctx* c = live_ctx(env, argv[0]);
+  if (!c) return nullptr;
+  napi_value d = argv[1], v;
+  std::vector<napi_value> bound;
+  auto tensor = [&](napi_value obj, const char* name, size_t min_bytes, const void** ptr, int64_t* bytes) {
+    if (!prop(env, obj, name, &v)) {
+      napi_throw_type_error(env, nullptr, (std::string("missing ") + name).c_str());
+      return false;
+    }
+    Buf* b = live_buf(env, v);
+    if (!b) return false;
+    if (b->owner != c) {
+      napi_throw_error(env, nullptr, (std::string(name) + " belongs to another context").c_str());
+      return false;
+    }
+    if (b->bytes < min_bytes) {
+      napi_throw_range_error(env, nullptr, (std::string(name) + " is smaller than its tensor").c_str());
+      return false;
+    }
+    *ptr = b->ptr;
+    if (bytes) *bytes = (int64_t)b->bytes;
+    bound.push_back(v);
+    return true;
+  };
+  auto num = [&](const char* name, double dflt) {
+    double x = dflt;
+    if (prop(env, d, name, &v)) napi_get_value_double(env, v, &x);
+    return x;
+  };
+  qattn_model_desc desc{};
+  const void* p = nullptr;
+  if (!tensor(d, "tokenEmbd", 0, &desc.token_embd, &desc.token_embd_bytes)) return nullptr;
+  if (!tensor(d, "outputNorm", 1024 * 4, &p, nullptr)) return nullptr;
+  desc.output_norm = static_cast<const float*>(p);
+  napi_value layers;
+  bool is_arr = false;
+  if (!prop(env, d, "layers", &layers) || napi_is_array(env, layers, &is_arr) != napi_ok || !is_arr) {
+    napi_throw_type_error(env, nullptr, "layers must be an array");
+    return nullptr;
+  }
+  uint32_t n = 0;
+  napi_get_array_length(env, layers, &n);
+  std::vector<qattn_layer_weights> lw(n);
+  for (uint32_t i = 0; i < n; ++i) {
+    napi_value l;
+    NAPI_OK(env, napi_get_element(env, layers, i, &l));
+    qattn_layer_weights& w = lw[i];
+    const void *an, *qn, *kn, *fn;
+    if (!tensor(l, "attnNorm", 1024 * 4, &an, nullptr) || !tensor(l, "attnQNorm", 128 * 4, &qn, nullptr) ||
+        !tensor(l, "attnKNorm", 128 * 4, &kn, nullptr) || !tensor(l, "ffnNorm", 1024 * 4, &fn, nullptr) ||
+        !tensor(l, "attnQkv", 0, &w.attn_qkv, &w.attn_qkv_bytes) ||
+        !tensor(l, "attnOutput", 0, &w.attn_output, &w.attn_output_bytes) ||
+        !tensor(l, "ffnGateUp", 0, &w.ffn_gate_up, &w.ffn_gate_up_bytes) ||
+        !tensor(l, "ffnDown", 0, &w.ffn_down, &w.ffn_down_bytes))
+      return nullptr;
+    w.attn_norm = static_cast<const float*>(an);
+    w.attn_q_norm = static_cast<const float*>(qn);
+    w.attn_k_norm = static_cast<const float*>(kn);
+    w.ffn_norm = static_cast<const float*>(fn);
+  }
+  desc.n_layers = (int32_t)n;
+  desc.layers = lw.data();
+  desc.eps = num("eps", 1e-6);
+  desc.rope_theta = num("ropeTheta", 1e6);
+  desc.mask = (int32_t)num("mask", QATTN_MASK_PREFIX_LOCAL);
+  desc.prefix = (int32_t)num("prefix", 176);
+  desc.window = (int32_t)num("window", 432);
+  bool invariant = true;
+  if (prop(env, d, "batchInvariant", &v)) napi_get_value_bool(env, v, &invariant);
+  desc.flags = invariant ? QATTN_FLAG_BATCH_INVARIANT : 0;
+  qattn_model* model = nullptr;
+  int rc = qattn_model_create(c->ctx, &desc, &model);
+  if (rc) return throw_qattn(env, rc, c->ctx);
+  auto* m = new Model{c, model, {}, {}};
+  for (napi_value b : bound) {
+    napi_ref ref;
+    NAPI_OK(env, napi_create_reference(env, b, 1, &ref));
+    m->bound_refs.push_back(ref);
+  }
+  c->models.insert(m);
+  ++c->refs;
+  napi_value out;
+  NAPI_OK(env, napi_create_external(env, m, finalize_model, nullptr, &out));
+  return out;
+}
+
+Model* live_model(napi_env env, napi_value v) {
+  Model* m = get_external<Model>(env, v, "model");
+  if (m && (!m->model || !m->owner->ctx)) {
+    napi_throw_error(env, nullptr, "model was destroyed");
+    return nullptr;
+  }
+  return m;
+}
+
+napi_value DestroyModel(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!args_of(env, info, 1, argv)) return nullptr;
+  Model* m = get_external<Model>(env, argv[0], "model");
+  if (!m) return nullptr;
+  if (m->owner->ctx) {
+    drop_model_plans(m);
+    if (m->model) qattn_model_destroy(m->model);
+  }
+  m->model = nullptr;
+  return undefined(env);
+}
+
+// createModelPlan(model, maxTokens, maxSeqs) -> external
+napi_value CreateModelPlan(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  if (!args_of(env, info, 3, argv)) return nullptr;
+  Model* m = live_model(env, argv[0]);
+  if (!m) return nullptr;
+  int64_t max_tokens = 0, max_seqs = 0;
+  if (!get_i64(env, argv[1], &max_tokens) || !get_i64(env, argv[2], &max_seqs) || max_tokens < 1 ||
+      max_tokens > INT32_MAX || max_seqs < 1 || max_seqs > QATTN_MAX_SEQS) {
+    napi_throw_range_error(env, nullptr, "maxTokens / maxSeqs out of range");
+    return nullptr;
+  }
+  qattn_model_plan* plan = nullptr;
+  int rc = qattn_model_plan_create(m->model, (int32_t)max_tokens, (int32_t)max_seqs, &plan);
+  if (rc) return throw_qattn(env, rc, m->owner->ctx);
+  auto* p = new Plan{m->owner, m, plan, nullptr, max_tokens, max_seqs};
+  NAPI_OK(env, napi_create_reference(env, argv[0], 1, &p->model_ref));
+  m->plans.insert(p);
+  m->owner->plans.insert(p);
+  ++m->owner->refs;
+  napi_value out;
+  NAPI_OK(env, napi_create_external(env, p, finalize_plan, nullptr, &out));
+  return out;
+}
+
+Plan* live_plan(napi_env env, napi_value v) {
+  Plan* p = get_external<Plan>(env, v, "model plan");
+  if (p && (!p->plan || !p->owner->ctx)) {
+    napi_throw_error(env, nullptr, "model plan was destroyed");
+    return nullptr;
+  }
+  return p;
+}
+
+napi_value DestroyModelPlan(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!args_of(env, info, 1, argv)) return nullptr;
+  Plan* p = get_external<Plan>(env, argv[0], "model plan");
+  if (!p) return nullptr;
+  if (p->plan && p->owner->ctx) qattn_model_plan_destroy(p->plan);
+  p->plan = nullptr;
+  return undefined(env);
+}
+
+// runModelPlan(plan, ids, cuSeqlens, out) / profileModelPlan(...) -> {stage: ms}: one packed batch
+// (ids Int32Array / Uint32Array of cuSeqlens[nseq] token ids) into the f32 [nseq][1024] device
+// buffer `out`; enqueued on the context stream (profile waits for it).
+napi_value ModelPlanCommon(napi_env env, napi_callback_info info, bool profile) {
+  napi_value argv[4];
+  if (!args_of(env, info, 4, argv)) return nullptr;
+  Plan* p = live_plan(env, argv[0]);
+  if (!p) return nullptr;
+  std::vector<int32_t> ids, cu;
+  if (!get_i32_array(env, argv[1], &ids) || !get_i32_array(env, argv[2], &cu) || cu.size() < 2) {
+    napi_throw_type_error(env, nullptr, "ids and cuSeqlens must be Int32Array / Uint32Array / arrays");
+    return nullptr;
+  }
+  Buf* out = live_buf(env, argv[3]);
+  if (!out) return nullptr;
+  const int64_t nseq = (int64_t)cu.size() - 1;
+  if (out->owner != p->owner || out->bytes < (size_t)nseq * 1024 * 4) {
+    napi_throw_range_error(env, nullptr, "out must be a buffer of this context holding nseq x 1024 f32");
+    return nullptr;
+  }
+  if (cu.back() < 0 || (size_t)cu.back() > ids.size()) {
+    napi_throw_range_error(env, nullptr, "ids holds fewer tokens than cuSeqlens[nseq]");
+    return nullptr;
+  }
+  qattn_ctx* ctx = p->owner->ctx;
+  if (!profile) {
+    int rc = qattn_model_plan_run(p->plan, ids.data(), cu.data(), (int32_t)nseq, static_cast<float*>(out->ptr), 1024,
+                                  nullptr);
+    if (rc) return throw_qattn(env, rc, ctx);
+    return undefined(env);
+  }
+  float ms[QATTN_STAGE_COUNT];
+  int rc = qattn_model_plan_profile(p->plan, ids.data(), cu.data(), (int32_t)nseq, static_cast<float*>(out->ptr), 1024,
+                                    nullptr, ms);
+  if (rc) return throw_qattn(env, rc, ctx);
+  static const char* names[QATTN_STAGE_COUNT] = {"embedding_norm",      "qkv",         "rope_attention",
+                                                 "attention_output",    "post_attention_norm",
+                                                 "ffn_up_gate",         "swiglu",      "ffn_down",
+                                                 "post_ffn_norm",       "pool"};
+  napi_value o;
+  NAPI_OK(env, napi_create_object(env, &o));
+  for (int s = 0; s < QATTN_STAGE_COUNT; ++s) {
+    napi_value x;
+    NAPI_OK(env, napi_create_double(env, ms[s], &x));
+    NAPI_OK(env, napi_set_named_property(env, o, names[s], x));
+  }
+  return o;
+}
+napi_value RunModelPlan(napi_env env, napi_callback_info info) { return ModelPlanCommon(env, info, false); }
+napi_value ProfileModelPlan(napi_env env, napi_callback_info info) { return ModelPlanCommon(env, info, true); }
+
 napi_value Synchronize(napi_env env, napi_callback_info info) {
   napi_value argv[1];
   if (!args_of(env, info, 1, argv)) return nullptr;
@@ -889,6 +1164,9 @@ napi_value Init(napi_env env, napi_value exports) {
       {"qkNormRopeQkv", QkNormRopeQkv}, {"updateRun", UpdateRun},
       {"poolLastL2", PoolLastL2},     {"q4Matmul", Q4Matmul},
       {"synchronize", Synchronize},   {"synchronizeAsync", SynchronizeAsync},
+      {"createModel", CreateModel},   {"destroyModel", DestroyModel},
+      {"createModelPlan", CreateModelPlan}, {"destroyModelPlan", DestroyModelPlan},
+      {"runModelPlan", RunModelPlan}, {"profileModelPlan", ProfileModelPlan},
   };
   for (const Fn& f : fns) {
     napi_value fn;

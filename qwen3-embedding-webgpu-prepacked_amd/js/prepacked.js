@@ -30,7 +30,7 @@ const GGML_Q40_BYTES = 18;  // one GGML Q4_0 block: f16 scale + 16 quant bytes
 const STORAGE_COMPACT = 'q4_0-tile32-compact';
 const STORAGE_RAW = 'raw';
 // GGML tensor type ids used here (the reference's src/gguf/types.ts enum).
-const GGML_TYPE = Object.freeze({ F32: 0, F16: 1, Q4_0: 2 });
+const GGML_TYPE = Object.freeze({ F32: 0, F16: 1, Q4_0: 2, Q6_K: 14 });
 
 class PrepackedFormatError extends Error {
   constructor(code, message) {

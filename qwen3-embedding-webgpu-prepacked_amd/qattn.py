@@ -82,6 +82,7 @@ class ModelDesc(ctypes.Structure):
         ("layers", ctypes.POINTER(LayerWeights)),
         ("eps", ctypes.c_double), ("rope_theta", ctypes.c_double),
         ("mask", ctypes.c_int32), ("prefix", ctypes.c_int32), ("window", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
     ]
 
 
@@ -439,17 +440,17 @@ class Context:
                self.handle)
 
     def model(self, token_embd, output_norm, layers, eps=1e-6, rope_theta=1e6, mask=MASK_PREFIX_LOCAL,
-              prefix=176, window=432):
+              prefix=176, window=432, flags=0):
         """qattn_model_create over device tensors: token_embd = (ptr, bytes), output_norm = ptr,
         layers = list of dicts with the LayerWeights field names (compact tensors as (ptr, bytes))."""
-        return Model(self, token_embd, output_norm, layers, eps, rope_theta, mask, prefix, window)
+        return Model(self, token_embd, output_norm, layers, eps, rope_theta, mask, prefix, window, flags)
 
 
 class Model:
     """The weights of the forward (Qwen3WebGPUModel, model.ts:185-255); plan() makes an
     execution plan (Qwen3ExecutionPlan, model.ts:49-183)."""
 
-    def __init__(self, ctx, token_embd, output_norm, layers, eps, rope_theta, mask, prefix, window):
+    def __init__(self, ctx, token_embd, output_norm, layers, eps, rope_theta, mask, prefix, window, flags):
         self.ctx = ctx
         arr = (LayerWeights * len(layers))()
         for i, lw in enumerate(layers):
@@ -460,7 +461,7 @@ class Model:
                 setattr(arr[i], name, ptr)
                 setattr(arr[i], name + "_bytes", nbytes)
         d = ModelDesc(token_embd[0], token_embd[1], output_norm, len(layers),
-                      ctypes.cast(arr, ctypes.POINTER(LayerWeights)), eps, rope_theta, mask, prefix, window)
+                      ctypes.cast(arr, ctypes.POINTER(LayerWeights)), eps, rope_theta, mask, prefix, window, flags)
         h = ctypes.c_void_p()
         _check(lib().qattn_model_create(ctx.handle, ctypes.byref(d), ctypes.byref(h)), ctx.handle)
         self.handle = h

@@ -1,0 +1,47 @@
+'use strict';
+// GPU check of the Node model path, run by tests/test_gpu_js.py: a .wgpack (written by the test)
+// -> parsePrepackedModel -> HipQwen3Runtime -> Qwen3EmbeddingEngine.embed() for every request at
+// once (one micro-batch) -> emb.bin for the Python side to compare with the forward oracle.  Also
+// checks here: a request embedded alone gives bitwise what it gave inside the batch, and a
+// plan's profile() names the reference's stages.
+const fs = require('fs');
+const path = require('path');
+const assert = require('assert');
+const { Qwen3EmbeddingEngine, HipQwen3Runtime, prepacked } = require('../../qwen3-embedding-webgpu-prepacked_amd/js');
+const { STAGES } = require('../../qwen3-embedding-webgpu-prepacked_amd/js/model');
+
+async function main() {
+  const dir = process.argv[2];
+  const file = fs.readFileSync(path.join(dir, 'model.wgpack'));
+  const model = prepacked.parsePrepackedModel(file.buffer.slice(file.byteOffset, file.byteOffset + file.byteLength));
+  const { eos, lists } = JSON.parse(fs.readFileSync(path.join(dir, 'requests.json'), 'utf8'));
+  const runtime = new HipQwen3Runtime({ prepacked: model });
+  assert.strictEqual(runtime.model.layers, 2);
+  // text "3,17,5" -> token ids [3, 17, 5], the shape transformers.js returns (main.ts:191-199)
+  const tokenizer = (text) => ({ input_ids: { tolist: () => [text.split(',').map(Number)] } });
+  const engine = new Qwen3EmbeddingEngine(runtime, tokenizer, 16, 0, eos);
+  const outs = await Promise.all(lists.map((ids) => engine.embed(ids.join(','))));
+  const flat = new Float32Array(outs.length * 1024);
+  outs.forEach((o, i) => flat.set(o, i * 1024));
+  fs.writeFileSync(path.join(dir, 'emb.bin'), Buffer.from(flat.buffer));
+
+  const alone = await engine.embed(lists[1].join(','));
+  assert.ok(alone.every((x, i) => x === outs[1][i]), 'a request alone differs from the same request in a batch');
+
+  const plan = runtime.model.createPlan(2, 256);
+  const ids = Uint32Array.from(lists[0].concat(lists[1]));
+  const stages = plan.profile(ids, [lists[0].length, lists[1].length]);
+  assert.deepStrictEqual(Object.keys(stages), STAGES);
+  assert.ok(Object.values(stages).every((ms) => ms > 0));
+  assert.throws(() => plan.profile(Uint32Array.from([0, 1]), [3]), /token buffer/);
+  const [e0] = await plan.run(Uint32Array.from(lists[1]), [lists[1].length]);
+  assert.ok(e0.every((x, i) => x === outs[1][i]), 'plan.run differs from the engine');
+  plan.destroy();
+  runtime.destroy();
+  console.log(JSON.stringify({ ok: true, requests: outs.length, stages }));
+}
+
+main().catch((e) => {
+  console.error(e);
+  process.exit(1);
+});

@@ -33,3 +33,30 @@ def test_node_gpu_path(oracle, tmp_path):
     cos = ((o * exact).sum(-1) / (np.linalg.norm(o, axis=-1) * np.linalg.norm(exact, axis=-1))).min()
     print(f"node path: max|err| {err:.3e} min cos {cos:.7f}")
     assert err <= 2e-3 and cos >= 0.9999
+
+
+@pytest.mark.skipif(shutil.which("node") is None, reason="node is not installed")
+def test_node_model_path(tmp_path):
+    """The whole forward through Node: a synthetic 2-layer .wgpack, the engine's micro-batch of
+    ragged requests, embeddings against the forward oracle (same bar as test_gpu_model)."""
+    import json
+
+    import model_ref as mr
+    import wgpack
+    weights = mr.synthetic_weights(31, 2, vocab=300)
+    wgpack.write_model(str(tmp_path / "model.wgpack"), weights)
+    rng = np.random.default_rng(12)
+    eos = 299
+    lists = [rng.integers(0, eos, n).tolist() + [eos] for n in (3, 40, 129, 6, 200)]
+    (tmp_path / "requests.json").write_text(json.dumps({"eos": eos, "lists": lists}))
+    r = subprocess.run(["node", os.path.join(HERE, "js", "model.gpu.js"), str(tmp_path)],
+                       capture_output=True, text=True, timeout=180)
+    print(r.stdout, r.stderr[-2000:])
+    assert r.returncode == 0, r.stdout + r.stderr
+    got = np.fromfile(str(tmp_path / "emb.bin"), dtype=np.float32).reshape(len(lists), 1024)
+    cu = np.concatenate([[0], np.cumsum([len(t) for t in lists])]).astype(np.int32)
+    want = mr.forward(weights, np.concatenate(lists).astype(np.int32), cu)
+    err = np.abs(got - want).max()
+    cos = (np.sum(got * want, axis=1) / (np.linalg.norm(got, axis=1) * np.linalg.norm(want, axis=1))).min()
+    print(f"node model path: max|err| {err:.3e} min cos {cos:.7f}")
+    assert err <= 2e-3 and cos >= 0.9999

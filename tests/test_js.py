@@ -93,3 +93,11 @@ def test_bench_config1_lengths_equal_the_oracle_generator(oracle):
     bench = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(bench)
     assert bench.config1_lengths() == oracle.gen_lengths(oracle.seed(1, 0, 3), 16).tolist()
+
+
+@pytest.mark.skipif(shutil.which("node") is None, reason="node is not installed")
+def test_node_model_loader():
+    r = subprocess.run(["node", os.path.join(HERE, "js", "model.test.js")], capture_output=True,
+                       text=True, timeout=120)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
