@@ -417,7 +417,7 @@ def retained_pairs_sparse(L, prefix=176, window=432):
     return n * (n + 1) // 2 + max(0, L - prefix - window) * (prefix + window)
 
 
-def model_timing(reps):
+def model_timing(reps, names=("full", "sparse", "cfg4", "cfg1", "cfg3")):
     """The whole 28-layer forward (f4; not the headline metric): qattn_model_plan_run -- embedding
     lookup, 28 x (norms, four Q4_0 projections, QK-norm + RoPE, attention, SwiGLU), pool -- on
     synthetic weights at the BASELINE packings, random token ids over the full vocabulary.
@@ -429,7 +429,7 @@ def model_timing(reps):
     model, bufs = synthetic_model(ctx, q, LAYERS, MODEL_VOCAB)
     rng = np.random.default_rng(1)
     gemm_flop_per_token = 2.0 * (1024 * 4096 + 2048 * 1024 + 1024 * 6144 + 3072 * 1024) * LAYERS
-    for name in ("full", "sparse", "cfg4", "cfg1", "cfg3"):
+    for name in names:
         lengths = lengths_of(name)
         cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
         T = int(cu[-1])
@@ -502,7 +502,10 @@ def main():
                     help="only time N runs of the whole 28-layer forward (synthetic weights) per config and exit")
     args = ap.parse_args()
     if args.model:
-        model_timing(args.model)
+        if args.workload == "both":
+            model_timing(args.model)
+        else:
+            model_timing(args.model, (args.workload,))
         return
     if args.rope:
         rope_timing(args.rope)

@@ -118,7 +118,7 @@ export class PrepackedFormatError extends Error {
 export const prepacked: {
   PrepackedFormatError: typeof PrepackedFormatError;
   MAGIC: 'WGPACK02'; LAYOUT: 'q4_0-tile32-compact-v2'; TILE_ROWS: 32; BLOCK_VALUES: 32; BLOCK_BYTES: 20;
-  STORAGE_COMPACT: 'q4_0-tile32-compact'; STORAGE_RAW: 'raw'; GGML_TYPE: { F32: 0; F16: 1; Q4_0: 2 };
+  STORAGE_COMPACT: 'q4_0-tile32-compact'; STORAGE_RAW: 'raw'; GGML_TYPE: { F32: 0; F16: 1; Q4_0: 2; Q6_K: 14 };
   packQ40Tile32(name: string, parts: ReadonlyArray<{ name: string; k: number; n: number; bytes: Uint8Array }>): PackedTensorBytes;
   rawTensor(name: string, dimensions: number[], type: number, bytes: Uint8Array): PackedTensorBytes;
   buildPrepackedFile(sourceSha256: string, sourceBytes: number,
@@ -134,4 +134,41 @@ export class CompactQ4Matmul {
   upload(model: PrepackedModel, name: string): CompactQ4Weight;
   run(x: DeviceBuffer, rows: number, weight: CompactQ4Weight, y: DeviceBuffer,
       options?: { inputStride?: number; outputStride?: number }): void;
+}
+
+// ---- the whole model (the reference's Qwen3WebGPUModel / Qwen3ExecutionPlan, model.ts:49-255).
+/** Stage names of a profiled run, in order (model.ts:157-168). */
+export type ModelStage = 'embedding_norm' | 'qkv' | 'rope_attention' | 'attention_output' | 'post_attention_norm'
+  | 'ffn_up_gate' | 'swiglu' | 'ffn_down' | 'post_ffn_norm' | 'pool';
+export interface HipModelOptions {
+  /** Attention mask of the forward (default 'prefix-local', 176 / 432). */
+  mask?: 'causal' | 'prefix-local'; prefix?: number; window?: number;
+  /** Default true: a request's embedding is bitwise the same alone or in any batch. */
+  batchInvariant?: boolean;
+}
+/** The weights of a parsed .wgpack on the device (Q6_K token_embd, f32 norms, 4 compact Q4_0
+ * projections per layer, 1..28 layers), checked by name, storage, type and shape. */
+export class HipQwen3Model {
+  constructor(context: DeviceContext, prepacked: PrepackedModel, options?: HipModelOptions);
+  readonly layers: number;
+  readonly vocab: number;
+  createPlan(batch: number, sequence: number): HipQwen3Plan;
+  destroy(): void;
+}
+export class HipQwen3Plan implements EmbeddingPlan {
+  /** Packed token ids (lengths[i] per request) -> one L2-normalised Float32Array(1024) per request. */
+  run(ids: Uint32Array | Int32Array, lengths: Uint32Array | number[]): Promise<Float32Array[]>;
+  /** One run with each stage timed: total ms per stage over all layers. */
+  profile(ids: Uint32Array | Int32Array, lengths: Uint32Array | number[]): Record<ModelStage, number>;
+  readonly timing: { hostMs: number; totalMs: number; tokens: number } | null;
+  destroy(): void;
+}
+/** EmbeddingRuntime over the model: give `prepacked` (a parsed .wgpack) or a `model`. */
+export class HipQwen3Runtime implements EmbeddingRuntime {
+  constructor(options: HipModelOptions & { prepacked?: PrepackedModel; model?: HipQwen3Model;
+                                           context?: DeviceContext; device?: number });
+  readonly packing: 'varlen';
+  readonly model: HipQwen3Model;
+  createPlan(batch: number, sequence: number): HipQwen3Plan;
+  destroy(): void;
 }
