@@ -33,6 +33,8 @@ hipError_t launch_fill_token_rows(half_t* dst, const int32_t* ids, int64_t rows,
                                   int64_t row_stride, uint64_t seed, hipStream_t stream);
 hipError_t launch_q4_matmul(const half_t* x, int64_t ldx, int M, int K, const uint8_t* w, uint32_t w_bytes, int N,
                             half_t* y, int64_t ldy, hipStream_t stream);
+hipError_t launch_q4_matmul_swiglu(const half_t* x, int64_t ldx, int M, int K, const uint8_t* w, uint32_t w_bytes,
+                                   int n_inter, half_t* y, int64_t ldy, hipStream_t stream);
 hipError_t launch_pool_last_l2(const half_t* x, int64_t row_stride, int width, const int32_t* cu_seqlens,
                                int nseq, float* out, int64_t out_row_stride, hipStream_t stream);
 }  // namespace qattn
@@ -710,14 +712,16 @@ int64_t qattn_q4_compact_bytes(int32_t K, int32_t N) {
   return (int64_t)((N + 31) / 32) * (K / 32) * 32 * 20;
 }
 
-int qattn_q4_matmul(qattn_ctx* ctx, const void* x, int64_t ldx, int32_t M, int32_t K, const void* w,
-                    int64_t w_bytes, int32_t N, void* y, int64_t ldy, qattn_stream_t stream) {
+namespace {
+// The checks both Q4_0 GEMM entry points share: N weight rows, y rows of at least `out_cols`.
+int check_q4_args(qattn_ctx* ctx, const void* x, int64_t ldx, int32_t M, int32_t K, const void* w, int64_t w_bytes,
+                  int32_t N, int32_t out_cols, const void* y, int64_t ldy) {
   if (!ctx || !x || !w || !y) return fail(ctx, QATTN_EINVAL, "ctx/x/w/y is NULL");
   if (M < 0 || N < 1 || K < 32 || K % 32)
     return fail(ctx, QATTN_EINVAL, "shape M=%d K=%d N=%d: M >= 0, N >= 1, K a positive multiple of 32", M, K, N);
-  if (ldx < K || ldx % 8 || ldy < N || ldy % 8)
-    return fail(ctx, QATTN_EINVAL, "ldx/ldy (%lld, %lld): >= K / N and multiples of 8 elements", (long long)ldx,
-                (long long)ldy);
+  if (ldx < K || ldx % 8 || ldy < out_cols || ldy % 8)
+    return fail(ctx, QATTN_EINVAL, "ldx/ldy (%lld, %lld): >= K / %d and multiples of 8 elements", (long long)ldx,
+                (long long)ldy, out_cols);
   const int64_t need = qattn_q4_compact_bytes(K, N);
   if (w_bytes < need || w_bytes > 0x7FFFFFFFll)
     return fail(ctx, QATTN_EINVAL, "w_bytes %lld: a %dx%d tile32-compact tensor holds %lld bytes (< 2 GiB)",
@@ -726,9 +730,30 @@ int qattn_q4_matmul(qattn_ctx* ctx, const void* x, int64_t ldx, int32_t M, int32
     return fail(ctx, QATTN_EINVAL, "x or y rows beyond 2 GiB (32-bit buffer offsets)");
   if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(y) % 16 || reinterpret_cast<uintptr_t>(w) % 4)
     return fail(ctx, QATTN_EINVAL, "x/y not 16-byte or w not 4-byte aligned");
+  return QATTN_OK;
+}
+}  // namespace
+
+int qattn_q4_matmul(qattn_ctx* ctx, const void* x, int64_t ldx, int32_t M, int32_t K, const void* w,
+                    int64_t w_bytes, int32_t N, void* y, int64_t ldy, qattn_stream_t stream) {
+  const int rc = check_q4_args(ctx, x, ldx, M, K, w, w_bytes, N, N, y, ldy);
+  if (rc != QATTN_OK) return rc;
   DeviceGuard g(ctx->device);
   HIP_TRY(ctx, launch_q4_matmul(static_cast<const half_t*>(x), ldx, M, K, static_cast<const uint8_t*>(w),
                                 (uint32_t)w_bytes, N, static_cast<half_t*>(y), ldy, pick_stream(ctx, stream)));
+  return QATTN_OK;
+}
+
+int qattn_q4_matmul_swiglu(qattn_ctx* ctx, const void* x, int64_t ldx, int32_t M, int32_t K, const void* w,
+                           int64_t w_bytes, int32_t n_inter, void* y, int64_t ldy, qattn_stream_t stream) {
+  if (n_inter < 64 || n_inter % 64 || n_inter > (1 << 29))
+    return fail(ctx, QATTN_EINVAL, "n_inter %d: a positive multiple of 64", n_inter);
+  const int rc = check_q4_args(ctx, x, ldx, M, K, w, w_bytes, 2 * n_inter, n_inter, y, ldy);
+  if (rc != QATTN_OK) return rc;
+  DeviceGuard g(ctx->device);
+  HIP_TRY(ctx, launch_q4_matmul_swiglu(static_cast<const half_t*>(x), ldx, M, K, static_cast<const uint8_t*>(w),
+                                       (uint32_t)w_bytes, n_inter, static_cast<half_t*>(y), ldy,
+                                       pick_stream(ctx, stream)));
   return QATTN_OK;
 }
 

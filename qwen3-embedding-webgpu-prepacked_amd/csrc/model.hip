@@ -48,7 +48,6 @@ struct qattn_model_plan {
   void* k = nullptr;           // roped K              [T][1024]
   void* attn = nullptr;        // attention output     [T][2048]
   void* delta = nullptr;       // projection output    [T][1024]
-  void* gate_up = nullptr;     // FFN gate | up        [T][6144]
   void* ffn = nullptr;         // SwiGLU output        [T][3072]
   qattn_run* run = nullptr;
   std::vector<int32_t> planned_cu;  // the batch the attention run is planned for
@@ -175,7 +174,7 @@ void free_plan(qattn_model_plan* p) {
   qattn_ctx* ctx = p->model->ctx;
   DeviceGuard g(ctx->device);
   (void)hipStreamSynchronize(ctx->stream);
-  void* bufs[] = {p->ids, p->x, p->normalized, p->qkv, p->q, p->k, p->attn, p->delta, p->gate_up, p->ffn};
+  void* bufs[] = {p->ids, p->x, p->normalized, p->qkv, p->q, p->k, p->attn, p->delta, p->ffn};
   for (void* b : bufs)
     if (b) (void)hipFree(b);
   delete p;
@@ -251,12 +250,13 @@ int enqueue(qattn_model_plan* p, const int32_t* cu, int32_t nseq, float* out, in
     STAGE_TRY(qattn_rmsnorm(ctx, p->x, kHidden, p->delta, kHidden, w.ffn_norm, p->normalized, kHidden, T, kHidden,
                             d.eps, s));
     end();
+    // The gate/up projection and SwiGLU are one launch (no [T][6144] intermediate); its time is
+    // the ffn_up_gate stage and the swiglu stage stays empty.
     begin(QATTN_STAGE_FFN_UP_GATE);
-    STAGE_TRY(qattn_q4_matmul(ctx, p->normalized, kHidden, (int32_t)T, kHidden, w.ffn_gate_up, w.ffn_gate_up_bytes,
-                              2 * kInter, p->gate_up, 2 * kInter, s));
+    STAGE_TRY(qattn_q4_matmul_swiglu(ctx, p->normalized, kHidden, (int32_t)T, kHidden, w.ffn_gate_up,
+                                     w.ffn_gate_up_bytes, kInter, p->ffn, kInter, s));
     end();
     begin(QATTN_STAGE_SWIGLU);
-    STAGE_TRY(qattn_swiglu(ctx, p->gate_up, 2 * kInter, p->ffn, kInter, T, kInter, s));
     end();
     begin(QATTN_STAGE_FFN_DOWN);
     STAGE_TRY(qattn_q4_matmul(ctx, p->ffn, kInter, (int32_t)T, kInter, w.ffn_down, w.ffn_down_bytes, kHidden, p->delta,
@@ -330,7 +330,7 @@ int qattn_model_plan_create(qattn_model* model, int32_t max_tokens, int32_t max_
                 {&p->normalized, T * kHidden * 2},             {&p->qkv, T * kQkvWidth * 2},
                 {&p->q, T * kQWidth * 2},                      {&p->k, T * kKWidth * 2},
                 {&p->attn, T * kQWidth * 2},                   {&p->delta, T * kHidden * 2},
-                {&p->gate_up, T * 2 * kInter * 2},             {&p->ffn, T * kInter * 2}};
+                {&p->ffn, T * kInter * 2}};
     for (const Buf& b : bufs) {
       const hipError_t e = hipMalloc(b.ptr, b.bytes);
       if (e != hipSuccess) {

@@ -18,6 +18,19 @@ hipError_t launch_embed_q6k(const int32_t* ids, int64_t tokens, const uint8_t* t
 hipError_t launch_rmsnorm(half_t* x, const half_t* residual, const float* weight, half_t* out, int64_t rows,
                           int width, int64_t x_stride, int64_t r_stride, int64_t out_stride, float eps,
                           hipStream_t stream);
+// silu(g) * u in fp32, rounded to fp16: the one formula of swiglu_kernel and of the fused
+// gate/up projection (q4_matmul.hip), so the two paths agree bit for bit.  The hardware exp2 and
+// reciprocal (about 1 fp32 ulp each) are far inside the fp16 rounding of the result.
+__device__ inline half_t swiglu_value(half_t g, half_t u) {
+  const float gf = (float)g;
+  float v = gf * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(gf * -1.44269504f)) * (float)u;
+  // The product is rounded to fp32 and then to fp16 in every caller: without this the compiler
+  // may fold the multiply and the conversion into one v_fma_mix (a single rounding) in one
+  // kernel and not in another.
+  asm volatile("" : "+v"(v));
+  return (half_t)v;
+}
+
 // out = silu(gate) * up for rows of [gate (width) | up (width)], width a multiple of 8.
 hipError_t launch_swiglu(const half_t* gate_up, int64_t gu_stride, half_t* out, int64_t out_stride, int64_t rows,
                          int width, hipStream_t stream);

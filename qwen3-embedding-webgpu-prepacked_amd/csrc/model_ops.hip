@@ -121,10 +121,7 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const half_t* gate_up, int6
   const h8 u = *reinterpret_cast<const h8*>(gate_up + r * gu_stride + width + c);
   h8 o;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float gf = (float)g[e];
-    o[e] = (_Float16)(gf / (1.f + expf(-gf)) * (float)u[e]);
-  }
+  for (int e = 0; e < 8; ++e) o[e] = swiglu_value(g[e], u[e]);
   *reinterpret_cast<h8*>(out + r * out_stride + c) = o;
 }
 

@@ -27,6 +27,8 @@
 
 #include <type_traits>
 
+#include "model_ops.h"
+
 namespace qattn {
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -74,6 +76,11 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 constexpr int kQ4TileBytes = kQ4Tile * 64;  // 8 KiB
 __device__ inline uint32_t q4_lds_off(int row, int chunk) { return row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4); }
 
+// SWIGLU: the weight is [gate (N/2 rows) | up (N/2 rows)] and the output is silu(gate) * up, N/2
+// columns: the workgroup of tile column tn takes gate rows 64 tn .. +63 and the matching up rows
+// (B rows 0-31 gate, 32-63 up, 64-95 gate, 96-127 up), so every wave holds the gate and up
+// accumulators of the same 32 features in the same lanes and applies swiglu_value to them.
+template <bool SWIGLU>
 __global__ __launch_bounds__(256, 2) void q4_matmul_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, int K,
                                                            const uint8_t* __restrict__ w, uint32_t w_bytes, int N,
                                                            _Float16* __restrict__ y, int64_t ldy, int tiles_n,
@@ -125,8 +132,8 @@ __global__ __launch_bounds__(256, 2) void q4_matmul_kernel(const _Float16* __res
   // of (n0 + n, kb): their low nibbles are columns 8h .. +7 (chunk h), their high nibbles columns
   // 16 + 8h .. +7 (chunk 2 + h).  Records of rows past the tensor read as zeros.
   const int brow = tid >> 1, bhalf = tid & 1;
-  const uint32_t w_rec = ((uint32_t)((n0 + brow) >> 5) * (uint32_t)kblocks * 32u + (uint32_t)((n0 + brow) & 31)) *
-                         kQ4Record;
+  const int wtile = SWIGLU ? ((brow >> 5) & 1 ? N >> 6 : 0) + (n0 >> 6) + (brow >> 6) : (n0 + brow) >> 5;
+  const uint32_t w_rec = ((uint32_t)wtile * (uint32_t)kblocks * 32u + (uint32_t)(brow & 31)) * kQ4Record;
   const uint32_t w_step = 32u * kQ4Record;
   const uint32_t b_lo = q4_lds_off(brow, bhalf), b_hi = q4_lds_off(brow, 2 + bhalf);
   struct WRegs {
@@ -222,6 +229,20 @@ __global__ __launch_bounds__(256, 2) void q4_matmul_kernel(const _Float16* __res
   // D (32 x 32 per block): lane holds column l32 and rows 8 (r / 4) + 4 hl + r % 4, r = 0..15.
   // Columns >= N are skipped here; rows >= M fall outside the Y resource and are dropped.
   const int wm = m0 + wr, wn = n0 + wc;
+  if constexpr (SWIGLU) {
+    // Block nb = 0 holds gate, nb = 1 up, of output features (n0 + wc) / 2 + l32.
+    const uint32_t n = (uint32_t)((wn >> 1) + l32);
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = wm + 32 * mb + 8 * (r >> 2) + 4 * hl + (r & 3);
+        const uint32_t off = m < M ? ((uint32_t)m * (uint32_t)ldy + n) * 2u : 0x80000000u;
+        const _Float16 v = swiglu_value((_Float16)acc[mb][0][r], (_Float16)acc[mb][1][r]);
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), yrs, off, 0, 0);
+      }
+    return;
+  }
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
     const int n = wn + 32 * nb + l32;
@@ -245,8 +266,21 @@ hipError_t launch_q4_matmul(const _Float16* x, int64_t ldx, int M, int K, const 
   if (M <= 0 || N <= 0) return hipSuccess;
   const int tiles_m = (M + kQ4Tile - 1) / kQ4Tile, tiles_n = (N + kQ4Tile - 1) / kQ4Tile;
   const int tiles = tiles_m * tiles_n, per_xcd = (tiles + 7) / 8;
-  hipLaunchKernelGGL(q4_matmul_kernel, dim3((unsigned)(8 * per_xcd)), dim3(256), 0, stream, x, ldx, M, K, w, w_bytes,
-                     N, y, ldy, tiles_n, tiles, per_xcd);
+  hipLaunchKernelGGL(q4_matmul_kernel<false>, dim3((unsigned)(8 * per_xcd)), dim3(256), 0, stream, x, ldx, M, K, w,
+                     w_bytes, N, y, ldy, tiles_n, tiles, per_xcd);
+  return hipGetLastError();
+}
+
+// y [M, n_inter] = swiglu of the [gate | up] projection; the weight has 2 n_inter rows and
+// n_inter is a multiple of 64.
+hipError_t launch_q4_matmul_swiglu(const _Float16* x, int64_t ldx, int M, int K, const uint8_t* w, uint32_t w_bytes,
+                                   int n_inter, _Float16* y, int64_t ldy, hipStream_t stream) {
+  if (M <= 0 || n_inter <= 0) return hipSuccess;
+  const int N = 2 * n_inter;
+  const int tiles_m = (M + kQ4Tile - 1) / kQ4Tile, tiles_n = N / kQ4Tile;
+  const int tiles = tiles_m * tiles_n, per_xcd = (tiles + 7) / 8;
+  hipLaunchKernelGGL(q4_matmul_kernel<true>, dim3((unsigned)(8 * per_xcd)), dim3(256), 0, stream, x, ldx, M, K, w,
+                     w_bytes, N, y, ldy, tiles_n, tiles, per_xcd);
   return hipGetLastError();
 }
 

@@ -138,6 +138,7 @@ def lib():
         "qattn_pool_last_l2": (ctypes.c_int, [vp, vp, i64, i32, vp, i32, vp, i64, vp]),
         "qattn_q4_compact_bytes": (i64, [i32, i32]),
         "qattn_q4_matmul": (ctypes.c_int, [vp, vp, i64, i32, i32, vp, i64, i32, vp, i64, vp]),
+        "qattn_q4_matmul_swiglu": (ctypes.c_int, [vp, vp, i64, i32, i32, vp, i64, i32, vp, i64, vp]),
         "qattn_fill_normal": (ctypes.c_int, [vp, vp, i64, i64, i64, ctypes.c_uint64, vp]),
         "qattn_fill_token_rows": (ctypes.c_int, [vp, vp, vp, i64, i64, i64, ctypes.c_uint64, vp]),
         "qattn_gen_qkv": (ctypes.c_int, [vp, ctypes.c_uint32, ctypes.c_uint32, vp, i32,
@@ -398,6 +399,13 @@ class Context:
         """y = x W^T for tile32-compact Q4_0 weights W [N, K] (quant-matmul.ts:267-307)."""
         _check(lib().qattn_q4_matmul(self.handle, x_ptr, K if ldx is None else ldx, M, K, w_ptr, w_bytes, N,
                                      y_ptr, N if ldy is None else ldy, stream), self.handle)
+
+    def q4_matmul_swiglu(self, x_ptr, M, K, w_ptr, w_bytes, n_inter, y_ptr, ldx=None, ldy=None, stream=None):
+        """y = swiglu(x W^T) for a [gate (n_inter rows) | up (n_inter rows)] tile32-compact Q4_0
+        weight, in one launch: the compact matmul of quant-matmul.ts:267-307 followed by
+        SwiGLUKernel (ops.ts:74-102), bit-identical to q4_matmul then swiglu."""
+        _check(lib().qattn_q4_matmul_swiglu(self.handle, x_ptr, K if ldx is None else ldx, M, K, w_ptr, w_bytes,
+                                            n_inter, y_ptr, n_inter if ldy is None else ldy, stream), self.handle)
 
     def fill_normal(self, ptr, rows, row_elems, row_stride, seed, stream=None):
         _check(lib().qattn_fill_normal(self.handle, ptr, rows, row_elems, row_stride, seed, stream),

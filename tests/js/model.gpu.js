@@ -32,7 +32,8 @@ async function main() {
   const ids = Uint32Array.from(lists[0].concat(lists[1]));
   const stages = plan.profile(ids, [lists[0].length, lists[1].length]);
   assert.deepStrictEqual(Object.keys(stages), STAGES);
-  assert.ok(Object.values(stages).every((ms) => ms > 0));
+  // the gate/up projection and SwiGLU are one launch, timed as ffn_up_gate; swiglu stays empty
+  assert.ok(Object.entries(stages).every(([k, ms]) => (k === 'swiglu' ? ms >= 0 : ms > 0)));
   assert.throws(() => plan.profile(Uint32Array.from([0, 1]), [3]), /token buffer/);
   const [e0] = await plan.run(Uint32Array.from(lists[1]), [lists[1].length]);
   assert.ok(e0.every((x, i) => x === outs[1][i]), 'plan.run differs from the engine');

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol(qattn):
 
 
 def test_abi_version(qattn):
-    assert qattn.lib().qattn_abi_version() == 5
+    assert qattn.lib().qattn_abi_version() == 6
 
 
 def test_create_without_gpu_fails_cleanly(qattn):
@@ -273,4 +273,5 @@ def test_consumer_and_projection_entry_points_reject_null_before_any_device_use(
     assert lib.qattn_pool_last_l2(None, FAKE, 1024, 1024, cu.ctypes.data, 1, FAKE, 1024, None) == qattn.EINVAL
     assert b"NULL" in lib.qattn_last_error(None)
     assert lib.qattn_q4_matmul(None, FAKE, 64, 4, 64, FAKE, 2560, 8, FAKE, 8, None) == qattn.EINVAL
+    assert lib.qattn_q4_matmul_swiglu(None, FAKE, 64, 4, 64, FAKE, 5120, 64, FAKE, 64, None) == qattn.EINVAL
     assert b"NULL" in lib.qattn_last_error(None)

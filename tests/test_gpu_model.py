@@ -188,7 +188,8 @@ def test_model_profile_stages(ctx, qattn, weights, dmodel):
         ref = out.read(np.float32, (2, 1024)).copy()
         ms = plan.profile(ids, cu, out.ptr)
         assert list(ms) == list(qattn.STAGES)
-        assert all(v > 0 for v in ms.values())
+        # the gate/up projection and SwiGLU are one launch, timed as ffn_up_gate; swiglu is empty
+        assert all(v > 0 for k, v in ms.items() if k != "swiglu") and ms["swiglu"] >= 0
         assert np.array_equal(out.read(np.float32, (2, 1024)), ref)
     finally:
         out.free()

@@ -1,5 +1,6 @@
 """GPU parity of the Q4_0 tile32-compact dequant-GEMM (qattn_q4_matmul, replacing the reference's
-compact batch matmul, src/webgpu/quant-matmul.ts:267-307) against the f64 oracle, through the C ABI.
+compact batch matmul, src/webgpu/quant-matmul.ts:267-307) against the f64 oracle, through the C ABI,
+and of its fused gate/up + SwiGLU form (qattn_q4_matmul_swiglu).
 
 Tolerance, per element: the fp32 sum of K exact products (f16 x f16 products are exact in fp32)
 errs by at most (K + 2) u32 * sum_k |x_k w_k| (u32 = 2^-24), and the final fp16 rounding by half an
@@ -92,6 +93,47 @@ def test_q4_matmul_reference_format_vector(ctx, oracle):
     assert np.array_equal(y[:, 1], [2 * (7 - (j & 15)) for j in range(32)])
 
 
+def run_q4_swiglu(ctx, x, packed, k, n_inter, ldy=None):
+    m = x.shape[0]
+    ldy = n_inter if ldy is None else ldy
+    bx, bw = ctx.upload(np.ascontiguousarray(x).view(np.uint16)), ctx.upload(packed)
+    by = ctx.alloc(max(m, 1) * ldy * 2)
+    by.fill_u16(0x7E00)
+    ctx.q4_matmul_swiglu(bx.ptr, m, k, bw.ptr, packed.size, n_inter, by.ptr, ldy=ldy)
+    ctx.synchronize()
+    y = by.read(np.uint16, (max(m, 1), ldy)).view(np.float16)
+    for b in (bx, bw, by):
+        b.free()
+    return y[:m]
+
+
+@pytest.mark.parametrize("m,k,n_inter", [(1, 32, 64), (130, 96, 128), (257, 1024, 3072)])
+def test_q4_matmul_swiglu_equals_the_two_launches(ctx, oracle, m, k, n_inter):
+    """The fused gate/up projection + SwiGLU (one launch) against the launches it replaces: the
+    projection into [m, 2 n_inter] (checked against the oracle's product here too), then
+    qattn_swiglu -- equal bit for bit -- and within one fp16 step of the f64 SwiGLU restatement
+    (oracle/model_ref.py, ops.ts:81-88) of that projection."""
+    import model_ref as mr
+    rng = np.random.default_rng(m + k + n_inter)
+    packed = random_compact(rng, 2 * n_inter, k)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    gate_up = run_q4(ctx, x, packed, k, 2 * n_inter)
+    check(oracle, gate_up, x, packed, k, 2 * n_inter, f"gate_up {m}x{k}x{2 * n_inter}")
+    dg, do = ctx.upload(np.ascontiguousarray(gate_up).view(np.uint16)), ctx.alloc(m * n_inter * 2)
+    ctx.swiglu(dg.ptr, do.ptr, m, width=n_inter)
+    ctx.synchronize()
+    two = do.read(np.uint16, (m, n_inter))
+    dg.free()
+    do.free()
+    fused = run_q4_swiglu(ctx, x, packed, k, n_inter, ldy=n_inter + 8)
+    assert np.isnan(fused[:, n_inter:].astype(np.float32)).all()  # columns past n_inter are not written
+    assert np.array_equal(fused[:, :n_inter].view(np.uint16), two)
+    ref = mr.swiglu(gate_up, n_inter).astype(np.float64)
+    got = fused[:, :n_inter].astype(np.float64)
+    step = np.maximum(np.spacing(np.maximum(np.abs(got), np.abs(ref)).astype(np.float16)).astype(np.float64), 2.0 ** -24)
+    assert (np.abs(got - ref) / step).max() <= 1
+
+
 def test_q4_matmul_invalid_arguments(ctx, qattn):
     buf = ctx.alloc(1 << 16)
     good = dict(m=4, k=64, n=8, w_bytes=qattn.lib().qattn_q4_compact_bytes(64, 8), ldx=64, ldy=8, x_off=0)
@@ -101,4 +143,11 @@ def test_q4_matmul_invalid_arguments(ctx, qattn):
             ctx.q4_matmul(buf.ptr + a["x_off"], a["m"], a["k"], buf.ptr, a["w_bytes"], a["n"], buf.ptr,
                           ldx=a["ldx"], ldy=a["ldy"])
         assert e.value.code == qattn.EINVAL, bad
+    # the fused entry point: n_inter a multiple of 64, y rows of n_inter, the weight 2 n_inter rows
+    w128 = qattn.lib().qattn_q4_compact_bytes(64, 128)
+    for n_inter, ldy, w_bytes in ((32, 64, w128), (96, 96, qattn.lib().qattn_q4_compact_bytes(64, 192)), (64, 56, w128),
+                                  (64, 64, w128 - 20)):
+        with pytest.raises(qattn.QattnError) as e:
+            ctx.q4_matmul_swiglu(buf.ptr, 4, 64, buf.ptr, w_bytes, n_inter, buf.ptr, ldy=ldy)
+        assert e.value.code == qattn.EINVAL, (n_inter, ldy, w_bytes)
     buf.free()
