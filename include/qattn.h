@@ -21,7 +21,7 @@
  *   EmbeddingLookupKernel (Q6_K)       ops.ts:381-423   | qattn_embed_q6k
  *   RmsNormKernel (residual + norm)    ops.ts:21-72     | qattn_rmsnorm
  *   SwiGLUKernel                       ops.ts:74-102    | qattn_swiglu
- *   gate/up matmul + SwiGLUKernel      model.ts:125-127 | qattn_q4_matmul_swiglu (fused)
+ *   gate/up matmul + SwiGLUKernel      model.ts:126-127 | qattn_q4_matmul_swiglu (fused)
  *   Qwen3WebGPUModel (weights)         model.ts:185-255 | qattn_model_create / _destroy
  *   Qwen3ExecutionPlan (28 layers)     model.ts:49-139  | qattn_model_plan_create / _run / _destroy
  *   Qwen3ExecutionPlan.profile()       model.ts:141-182 | qattn_model_plan_profile
@@ -262,7 +262,7 @@ int64_t qattn_q4_compact_bytes(int32_t K, int32_t N);
 int qattn_q4_matmul(qattn_ctx* ctx, const void* x, int64_t ldx, int32_t M, int32_t K, const void* w,
                     int64_t w_bytes, int32_t N, void* y, int64_t ldy, qattn_stream_t stream);
 /* The FFN's gate/up projection and SwiGLU in one launch (the reference runs its compact matmul
- * into a [T, 2 n_inter] buffer, then SwiGLUKernel, model.ts:125-127, ops.ts:74-102):
+ * into a [T, 2 n_inter] buffer, then SwiGLUKernel, model.ts:126-127, ops.ts:74-102):
  * y[m*ldy + j] = qattn_swiglu's value of (g, u) = (G[m][j], G[m][n_inter + j]) for j < n_inter,
  * where G is what qattn_q4_matmul writes for the 2 n_inter-row weight `w` (gate rows, then up
  * rows).  The same fp16 roundings and formula, so the result equals qattn_q4_matmul followed by

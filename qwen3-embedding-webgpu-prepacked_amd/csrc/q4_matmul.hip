@@ -1,5 +1,5 @@
 // q4_matmul.hip -- Q4_0 "tile32-compact" dequant-GEMM: Y = X W^T with fp16 activations X [M, K]
-// and 4-bit weights W [N, K], the projection that produces the attention path's Q/K/V rows.
+// and 4-bit weights W [N, K]: the model's four projections (QKV, attention output, gate/up, down).
 //
 // Replaces the reference's compact batch matmul (src/webgpu/quant-matmul.ts:267-307, dequant
 // :99-108) over the layout written by packQ40Tile32 (src/prepacked/format.ts:64-96): 20-byte
@@ -10,18 +10,22 @@
 //
 // The CDNA4 shape:
 //   * workgroup tile 128 (M) x 128 (N), four wavefronts of 64 x 64, each 2 x 2 blocks of
-//     v_mfma_f32_32x32x16_f16 with fp32 accumulators (64 VGPRs);
-//   * per 32-column K block a lane loads its A fragments straight from X (four 16-byte loads:
-//     rows of 32 consecutive halves are contiguous) and, for each of its two N blocks, one
-//     weight record's scale word and the 8 quant bytes its B fragment needs; the nibbles become
-//     f16 by bit-OR into 1024.0 (f16(1024 + q)), an exact subtract of 1032 and one f16 multiply
-//     by the scale (the same single rounding as the reference's f16 product);
-//   * a 4-stage register pipeline: the loads of K block kb + 3 are issued before block kb's 8
-//     MFMAs, into the stage that block kb - 1 just freed (stages are compile-time register sets,
-//     so nothing is copied, and every load is issued -- past the last block it re-reads the last
-//     block -- so the compiler's wait counts are the same on every path);
+//     v_mfma_f32_32x32x16_f16 with fp32 accumulators (64 VGPRs); 128 VGPRs in all, so up to four
+//     workgroups share a CU;
+//   * per 32-column K block: the X tile (128 rows x 64 B) goes HBM -> LDS by LDS-DMA
+//     (buffer_load ... lds, 16 B per lane); each weight record of the tile's 128 rows is read
+//     once (scale word + 8 quant bytes per thread) and dequantised into a B tile in LDS: the
+//     nibbles become f16 by bit-OR into 1024.0 (f16(1024 + q)), an exact subtract of 1032 and one
+//     f16 multiply by the scale (the same single rounding as the reference's f16 product);
+//   * both tiles are double-buffered with one barrier per K block, laid out with a 16-byte XOR
+//     swizzle so the fragment reads (ds_read_b128) are conflict free; the next block's
+//     fragments are read into a second register set right after the barrier, and the weight
+//     records are loaded three blocks ahead (clamped past the end, so every path issues the same
+//     loads and the wait counts are exact);
 //   * tiles are numbered so that consecutive workgroups on one XCD (workgroup b runs on XCD
-//     b % 8) walk the N tiles of one M tile: its X rows stay in that XCD's L2.
+//     b % 8) walk the N tiles of one M tile: its X rows stay in that XCD's L2;
+//   * the SWIGLU variant (the FFN's gate/up projection, model.ts:126-127) maps each workgroup's B
+//     rows onto a feature's gate and up rows and writes silu(gate) * up instead of the projection.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
