@@ -107,7 +107,7 @@ def run_q4_swiglu(ctx, x, packed, k, n_inter, ldy=None):
     return y[:m]
 
 
-@pytest.mark.parametrize("m,k,n_inter", [(1, 32, 64), (130, 96, 128), (257, 1024, 3072)])
+@pytest.mark.parametrize("m,k,n_inter", [(1, 32, 64), (130, 96, 128), (257, 1024, 3072), (1100, 256, 3072)])
 def test_q4_matmul_swiglu_equals_the_two_launches(ctx, oracle, m, k, n_inter):
     """The fused gate/up projection + SwiGLU (one launch) against the launches it replaces: the
     projection into [m, 2 n_inter] (checked against the oracle's product here too), then
