@@ -48,10 +48,11 @@ constexpr int kLoadsPerTile = kTileBytes / (kThreads * 16);  // 16 B per lane pe
 constexpr float kLazyLimit = 32768.f;
 
 
-// Partial result of one chunk of a split item, per wavefront: 17 records of 64 lanes x float4
-// (records 0..15: the lane's 64 O^T accumulators, 16: m, l, 0, 0), so every access is a
-// coalesced 1 KiB row.
-constexpr int kPartialRecords = 17;
+// Partial result of one chunk of a split item, per wavefront: 9 records of 64 lanes x 16 bytes
+// (record 2 db + h: the lane's O^T accumulators o[db][8h .. 8h+7] divided by the row's sum, as
+// fp16; record 8: m, the row's sum l, 0, 0 in fp32), so every access is a coalesced 1 KiB row.
+// fp16 is the output's own precision: the merge adds at most one more fp16 rounding per chunk.
+constexpr int kPartialRecords = 9;
 
 // Vector-memory instructions per lane that one item's prologue loads (Q: 8 x 16 B, K tiles 0
 // and 1: kLoadsPerTile each) and that one item's epilogue stores (O rows, 8 x 16 B, plus as many
@@ -96,6 +97,10 @@ __device__ inline uint32_t pack2(float a, float b) {
   const h2 v = {(half_t)a, (half_t)b};
   return __builtin_bit_cast(uint32_t, v);
 }
+
+// The low / high fp16 of a dword, widened (integer extraction, not a vector element).
+__device__ inline float half_lo(uint32_t d) { return (float)__builtin_bit_cast(half_t, (unsigned short)(d & 0xFFFFu)); }
+__device__ inline float half_hi(uint32_t d) { return (float)__builtin_bit_cast(half_t, (unsigned short)(d >> 16)); }
 
 // Record 0 of partial result `index` for (wave, lane); record r is 64 float4 further per r.
 __device__ inline float __attribute__((ext_vector_type(4)))* partial_records(float* partials, int index,
@@ -498,18 +503,26 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   // The item's last PV and its output rows.  O = O^T / l; lane pair (l, l^32) holds row q_pos,
   // dims 32db + 8g + 4hl + 0..3; one permlane32 swap per dword leaves each lane 8 consecutive
   // dims (16 B): g = 2gp in the low half-wave, g = 2gp+1 in the high one.
-  // Chunk of a split item: store this chunk's partial softmax state (per lane: O, m, l) for the
-  // merge kernel that runs after this launch; the chunk writes no output rows itself.
-  // kPartialRecords (>= kStoreOps) vector stores, so the next entry's wait stays correct.
+  // Chunk of a split item: store this chunk's partial softmax state (per lane: O / l, m, l) for
+  // the merge kernel that runs after this launch; the chunk writes no output rows itself.
+  // kPartialRecords vector stores; the next entry's first wait only ever waits for older ones.
   auto write_partial = [&](const WorkItem& w) {
     typedef float f4 __attribute__((ext_vector_type(4)));
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    const float l_tot = pair_sum(l_run);
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     f4* rec = partial_records(p.partials, (w.part >> 8) + (w.part & 15), wave, lane);
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
-        rec[64 * (4 * db + g)] = f4{o[db][4 * g], o[db][4 * g + 1], o[db][4 * g + 2], o[db][4 * g + 3]};
-    rec[64 * 16] = f4{m_run, l_run, 0.f, 0.f};
+      for (int gh = 0; gh < 2; ++gh) {
+        const f16x& v = o[db];
+        const int b = 8 * gh;
+        reinterpret_cast<u4*>(rec)[64 * (2 * db + gh)] =
+            u4{pack2(v[b] * inv, v[b + 1] * inv), pack2(v[b + 2] * inv, v[b + 3] * inv),
+               pack2(v[b + 4] * inv, v[b + 5] * inv), pack2(v[b + 6] * inv, v[b + 7] * inv)};
+      }
+    rec[64 * 8] = f4{m_run, l_tot, 0.f, 0.f};
   };
 
   using I0 = std::integral_constant<int, 0>;
@@ -569,10 +582,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
 
 // Merge of split items (after attn_fwd_kernel, same stream).  Workgroup (split item i, wave w)
 // redoes wavefront w's output rows of item i: thread 64 db + lane combines dims 32db..32db+31 of
-// lane's row -- records 4db..4db+3 of every chunk -- in chunk order: m = max_c m_c,
-// O = sum_c 2^(m_c - m) O_c, l likewise (a chunk with no key for the row has m_c = -inf and weighs
-// 0).  All of a thread's loads issue at once; the row sum pairs lanes l and l^32 as in the
-// attention kernel, so store_rows' layout applies per 32-dim block.
+// lane's row -- records 2db and 2db+1 of every chunk -- in chunk order: m = max_c m_c,
+// w_c = 2^(m_c - m) l_c, O = sum_c w_c (O/l)_c / sum_c w_c (a chunk with no key for the row has
+// m_c = -inf and weighs 0).  All of a thread's loads issue at once; store_rows' layout applies
+// per 32-dim block.  The fp16 halves are taken apart with integer shifts: hipcc has compiled the
+// element reads of a packed fp16 vector in an unrolled loop as element 0.
 constexpr int kMergeMaxChunks = 8;  // chunks merged per pass (more are folded in further passes)
 __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnParams p) {
   typedef float f4 __attribute__((ext_vector_type(4)));
@@ -585,15 +599,17 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnParams p) {
   const int nchunks = (w.part >> 4) & 15, first = w.part >> 8;
   float m = -INFINITY, l = 0.f;
   f4 acc[4] = {};
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
   for (int c0 = 0; c0 < nchunks; c0 += kMergeMaxChunks) {
-    f4 ml[kMergeMaxChunks], v[kMergeMaxChunks][4];
+    f4 ml[kMergeMaxChunks];
+    u4 v[kMergeMaxChunks][2];
 #pragma unroll
     for (int c = 0; c < kMergeMaxChunks; ++c) {
       if (c0 + c < nchunks) {
         const f4* rec = partial_records(p.partials, first + c0 + c, wave, lane);
-        ml[c] = rec[64 * 16];
+        ml[c] = rec[64 * 8];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) v[c][g] = rec[64 * (4 * db + g)];
+        for (int gh = 0; gh < 2; ++gh) v[c][gh] = reinterpret_cast<const u4*>(rec)[64 * (2 * db + gh)];
       }
     }
     float mp = m;
@@ -607,17 +623,21 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnParams p) {
 #pragma unroll
     for (int c = 0; c < kMergeMaxChunks; ++c) {
       if (c0 + c < nchunks) {
-        const float f = ml[c][0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml[c][0] - mp);
-        l += f * ml[c][1];
+        const float f = ml[c][0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml[c][0] - mp) * ml[c][1];
+        l += f;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) acc[g] += f * v[c][g];
+        for (int gh = 0; gh < 2; ++gh)
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            const uint32_t d0 = v[c][gh][2 * q], d1 = v[c][gh][2 * q + 1];
+            acc[2 * gh + q] += f * f4{half_lo(d0), half_hi(d0), half_lo(d1), half_hi(d1)};
+          }
       }
     }
     m = mp;
   }
   // Output: the block of dims 32db..32db+31 of this wave's rows, as store_rows lays them out.
-  const float l_tot = pair_sum(l);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  const float inv = l > 0.f ? 1.f / l : 0.f;  // l: the chunks' whole-row sums
   const int S = w.seq_len, head = (w.seq_kvh & 15) * kGroup + (wave >> 1);
   const int q_pos = w.q_block * kBlockQ + (wave & 1) * kWaveQ + lq;
   const uint32_t ostride_b = p.o_stride_b;

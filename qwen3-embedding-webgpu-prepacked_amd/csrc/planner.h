@@ -24,9 +24,10 @@ namespace qattn {
 constexpr int kXcds = 8;
 constexpr int kBlocksPerCU = 2;
 constexpr int kDefaultSlots = 256 * kBlocksPerCU;  // MI355X: 256 CUs
-// Partial result of one chunk: per wavefront (4) and lane (64), the 64 fp32 O^T accumulators
-// of the lane's row, then m and l (log2-domain row max, row sum) and two pad words.
-constexpr int kPartialFloats = 68;
+// Partial result of one chunk: per wavefront (4) and lane (64), the lane's 64 O^T values of its
+// row divided by the row sum, as fp16 (32 words), then m and l (log2-domain row max, row sum)
+// and two pad words.
+constexpr int kPartialFloats = 36;
 constexpr size_t kPartialBytes = (size_t)kWaves * 64 * kPartialFloats * 4;
 
 struct Plan {
