@@ -134,6 +134,25 @@ def test_q4_matmul_swiglu_equals_the_two_launches(ctx, oracle, m, k, n_inter):
     assert (np.abs(got - ref) / step).max() <= 1
 
 
+def test_q4_rows_do_not_depend_on_the_launch_shape(ctx, oracle):
+    """Launches with fewer than 256 tiles of 128x128 use 64-row workgroup tiles, larger ones
+    128-row tiles; every output element is computed the same way in both (the same K blocks and
+    MFMA order), so the first 64 rows alone equal the same rows of a 1100-row launch bit for bit
+    -- the model's batch invariance rests on this -- for the plain and the fused gate/up
+    projections."""
+    rng = np.random.default_rng(5)
+    k, n = 256, 4096
+    packed = random_compact(rng, n, k)
+    x = rng.standard_normal((1100, k)).astype(np.float16)
+    big = run_q4(ctx, x, packed, k, n)        # 9 x 32 = 288 tiles: 128-row tiles
+    small = run_q4(ctx, x[:64], packed, k, n)  # 1 x 32 tiles: 64-row tiles
+    check(oracle, big, x, packed, k, n, "q4 1100 rows")
+    assert np.array_equal(big[:64].view(np.uint16), small.view(np.uint16))
+    big_f = run_q4_swiglu(ctx, x, packed, k, n // 2)
+    small_f = run_q4_swiglu(ctx, x[:64], packed, k, n // 2)
+    assert np.array_equal(big_f[:64].view(np.uint16), small_f.view(np.uint16))
+
+
 def test_q4_matmul_invalid_arguments(ctx, qattn):
     buf = ctx.alloc(1 << 16)
     good = dict(m=4, k=64, n=8, w_bytes=qattn.lib().qattn_q4_compact_bytes(64, 8), ldx=64, ldy=8, x_off=0)
