@@ -60,3 +60,18 @@ def test_node_model_path(tmp_path):
     cos = (np.sum(got * want, axis=1) / (np.linalg.norm(got, axis=1) * np.linalg.norm(want, axis=1))).min()
     print(f"node model path: max|err| {err:.3e} min cos {cos:.7f}")
     assert err <= 2e-3 and cos >= 0.9999
+
+
+@pytest.mark.skipif(shutil.which("node") is None, reason="node is not installed")
+def test_engine_benchmark_script_runs():
+    """js/bench-engine.js (the engine's end-to-end timing on a synthetic model of the real
+    shapes) at 2 layers and one timed batch: both workloads report, with unit-norm embeddings."""
+    import json
+    script = os.path.join(HERE, "..", "qwen3-embedding-webgpu-prepacked_amd", "js", "bench-engine.js")
+    r = subprocess.run(["node", script, "2", "1"],
+                       capture_output=True, text=True, timeout=240)
+    print(r.stdout, r.stderr[-2000:])
+    assert r.returncode == 0, r.stdout + r.stderr
+    lines = [json.loads(l) for l in r.stdout.splitlines() if l.startswith("{")]
+    assert [l["workload"] for l in lines] == ["16x500", "1x5000"]
+    assert all(l["embeddings_unit_norm"] and l["requests_per_s"] > 0 for l in lines)
