@@ -101,3 +101,25 @@ def test_node_model_loader():
                        text=True, timeout=120)
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr
+
+
+@pytest.mark.skipif(shutil.which("node") is None, reason="node is not installed")
+def test_node_half_decode_is_ieee_binary16(tmp_path):
+    # runtime.js's binary16 -> f32 table (the decode of every result the Node runtime reads back)
+    # against numpy's IEEE conversion, on all 65,536 bit patterns: subnormals, signed zeros,
+    # infinities and NaNs included.
+    import numpy as np
+    mod = os.path.join(HERE, "..", "qwen3-embedding-webgpu-prepacked_amd", "js", "runtime.js")
+    out = tmp_path / "dec.bin"
+    script = (
+        f"const {{ halvesToFloat32 }} = require({mod!r});"
+        f"const bits = new Uint16Array(65536); for (let i = 0; i < 65536; i += 1) bits[i] = i;"
+        f"const f = halvesToFloat32(bits);"
+        f"require('fs').writeFileSync({str(out)!r}, Buffer.from(f.buffer));")
+    r = subprocess.run(["node", "-e", script], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr
+    got = np.frombuffer(out.read_bytes(), np.float32)
+    want = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))  # -0.0 kept
