@@ -44,6 +44,9 @@ int item_cost(int ntiles) { return 4 * ntiles + kEntryCost; }
 constexpr int kSlotBase = 18;
 constexpr int kChunkExtra = 0;
 constexpr int kMinChunkTiles = 2;
+// The merge kernel that follows a launch with split items (about 5 us, in cost units of a first
+// slot): a split plan must beat the best unsplit plan by more than this.
+constexpr int kMergeCost = 10;
 // Slot speeds, in time per unit of cost (per mille): slots cu_count..2*cu_count-1 (an XCD's
 // first 32 workgroups take one CU each) are the second workgroups.
 constexpr int64_t kFirstSlotTime = 1000;
@@ -276,6 +279,7 @@ void plan_work(const qattn_run_desc* d, int max_slots, Plan* out, qattn_run_info
     int64_t best_span = rounds(&best);
     best_span = improve(&best);
     int best_chunks = 0;
+    int64_t best_eff = best_span;  // makespan plus the merge kernel when the plan splits
     // Lower bound of the makespan: the total cost spread over the slots in proportion to their
     // speeds.  Targets step by a quarter tile (one cost unit) on a first slot.
     double rate = 0.0;
@@ -286,8 +290,10 @@ void plan_work(const qattn_run_desc* d, int max_slots, Plan* out, qattn_run_info
     for (int64_t T = lo; T <= lo + (4 * max_tiles + 8) * kFirstSlotTime && best_span > lo; T += kFirstSlotTime) {
       int nch = 0;
       const int64_t span = greedy(may_split ? T : INT64_MAX / 4, &trial, &nch);
-      if (span < best_span || (span == best_span && nch < best_chunks)) {
+      const int64_t eff = span + (nch ? (int64_t)kMergeCost * kFirstSlotTime : 0);
+      if (eff < best_eff || (eff == best_eff && nch < best_chunks)) {
         best_span = span;
+        best_eff = eff;
         best_chunks = nch;
         best.swap(trial);
       }

@@ -139,9 +139,14 @@ test('N-API addon loads; host-side planning and validation work without a GPU', 
   assert.strictEqual(plan.info.tokens, 550);
   assert.strictEqual(plan.info.pairs, 1275 + 125250);
   assert.strictEqual(plan.info.workItems, 8 * (1 + 8));
-  assert.strictEqual(plan.info.slots, 8 * 9);  // 9 items per KV head on 9 slots; long ones split
-  assert.ok(plan.items.length > plan.info.workItems * 8 && plan.info.splitItems > 0);
-  const inv = addon.planDescribe({ q: 1, k: 1, v: 1, o: 1, cuSeqlens: new Int32Array([0, 50, 550]), flags: 1 });
+  assert.strictEqual(plan.info.slots, 8 * 9);  // 9 items per KV head on 9 slots
+  // Splitting the 8-tile items would not pay for the merge kernel here: whole items.
+  assert.ok(plan.items.length === plan.info.workItems * 8 && plan.info.splitItems === 0);
+  // One 5,000-token sequence (79 items per KV head on 64 slots): long items are split.
+  const long = addon.planDescribe({ q: 1, k: 1, v: 1, o: 1, cuSeqlens: new Int32Array([0, 5000]) });
+  assert.strictEqual(long.info.slots, 512);
+  assert.ok(long.items.length > long.info.workItems * 8 && long.info.splitItems > 0);
+  const inv = addon.planDescribe({ q: 1, k: 1, v: 1, o: 1, cuSeqlens: new Int32Array([0, 5000]), flags: 1 });
   assert.strictEqual(inv.items.length, inv.info.workItems * 8);  // batch-invariant: whole items
   assert.strictEqual(inv.info.splitItems, 0);
   assert.throws(() => addon.planDescribe({ q: 1, k: 1, v: 1, o: 1, cuSeqlens: new Int32Array([0, 5, 3]) }), /non-decreasing/);

@@ -399,12 +399,16 @@ def test_split_k_and_batch_invariant_plans(ctx, qattn, oracle):
     # few fp16 ulps, and the batch-invariant rows equal the same sequence packed with others.
     cu = cu_of([5000])
     q, k, v = oracle.gen_qkv(5, 3, cu)
-    split = Case(ctx, qattn, q, k, v, cu)
+    split = Case(ctx, qattn, q, k, v, cu, o_last=True)
     whole = Case(ctx, qattn, q, k, v, cu, flags=qattn.FLAG_BATCH_INVARIANT)
-    assert qattn.plan_describe(split.desc)[1].split_items > 0
+    items, info = qattn.plan_describe(split.desc)
+    assert info.split_items > 0
+    # The last row's items are split too, so the merge kernel writes o_last (split + o_last).
+    assert any(it[2] == 4999 // 64 and it[6] >= 0 for it in items)
     assert qattn.plan_describe(whole.desc)[1].split_items == 0
     a, b = split.run(), whole.run()
     assert np.array_equal(a, split.run())  # split plans are deterministic
+    assert np.array_equal(split.last(), a[-1:])
     rows = np.arange(0, 5000, 7)
     exact = oracle.attention_exact(q, k, v, cu, rows=rows)
     compare(a[rows], exact, "1x5000 split-K")
