@@ -7,10 +7,12 @@ of independent seeded Q/K/V resident in HBM:
   * 1 x 5000 tokens, 176-prefix + 432-local sparse causal (the metric's sparse row)
 Every launch is one layer's attention through the C ABI (qattn_run_encode), exactly what the
 Node engine issues.  Timing: HIP events on the launch stream around exactly K steps, with a
-device synchronize on both sides.  A second pass brackets every launch with its own events to
-get each workload's average kernel duration -- for the headline workloads and, reported beside
-them in config.breakdown, for the other BASELINE configs (0: 1 x 50, 1: 16 ragged 10..150,
-3: 1 x 1500 sparse, 4: 4 x 5000 sparse with last-token rows).
+device synchronize on both sides.  A second pass brackets each workload's 28 back-to-back
+layer launches with one pair of events and divides by 28, to get the workload's average launch
+duration (the gaps between consecutive launches included, no event inside the sequence) -- for
+the headline workloads and, reported beside them in config.breakdown, for the other BASELINE
+configs (0: 1 x 50, 1: 16 ragged 10..150, 3: 1 x 1500 sparse, 4: 4 x 5000 sparse with
+last-token rows).
 
 cpu_baseline: the reference's tiled kernel (src/webgpu/ops.ts:168-241) restated in JavaScript
 (oracle/tiled16.js, f16 rounding points as the WGSL) and run under Node on this host's cores,
@@ -559,24 +561,25 @@ def main():
     ms_per_step = region_ms / args.steps
     log(f"timed {args.steps} steps: {region_ms:.3f} ms on device events ({host_ms:.3f} ms host)")
 
-    # ---- per-launch kernel durations (separate pass, same launches; the other configs too) ----
+    # ---- per-launch durations (separate pass, same launches; the other configs too): each
+    # workload's 28 layer launches back to back between one pair of events, / 28.  (An event pair
+    # around every single launch would add each event's own dispatch, 1-3 us per launch.) ----
     reps = max(3, min(args.steps, 10))
     per = {w.name: [] for w in wls + extra}
-    evs = [(ctx.event(), ctx.event()) for _ in range(LAYERS)]
+    ea, eb = ctx.event(), ctx.event()
     for w in extra:
         for _ in range(3):
             w.encode_all()
     for _ in range(reps):
         for w in wls + extra:
-            for r, (a, b) in zip(w.runs, evs):
-                a.record()
-                r.encode()
-                b.record()
             ctx.synchronize()
-            per[w.name] += [a.elapsed_ms(b) for a, b in evs]
-    for a, b in evs:
-        a.destroy()
-        b.destroy()
+            ea.record()
+            w.encode_all()
+            eb.record()
+            ctx.synchronize()
+            per[w.name].append(ea.elapsed_ms(eb) / len(w.runs))
+    ea.destroy()
+    eb.destroy()
 
     tokens_per_step = sum(w.tokens for w in wls) * LAYERS
     value = tokens_per_step / (ms_per_step / 1e3)

@@ -109,25 +109,29 @@ __device__ inline float __attribute__((ext_vector_type(4)))* partial_records(flo
   return reinterpret_cast<f4*>(partials) + ((size_t)index * kWaves + wave) * kPartialRecords * 64 + lane;
 }
 
-// Output rows of one wavefront: O = O^T / l for query row q_pos (lanes l and l^32 share it,
-// dims 32db + 8g + 4hl + 0..3), fp16, into O and (for the sequence's last row) o_last.  One
+// Output rows of one wavefront, staged through LDS.  O = O^T / l for query rows q_row0 ..
+// q_row0 + 31 (lanes l and l^32 hold row q_row0 + l % 32, dims 32db + 8g + 4hl + 0..3); one
 // permlane32 swap per dword leaves each lane 8 consecutive dims (16 B): g = 2gp in the low
-// half-wave, g = 2gp+1 in the high one.  Exactly kStoreOps<LAST> buffer stores per lane; rows past
-// the sequence (and every row but the last, for o_last) get an offset beyond the buffer resource,
-// so their stores are dropped (S * o stride < 2^31 is validated on the host).
-template <bool LAST>
-__device__ inline void store_rows(const AttnParams& p, const f16x (&o)[4], float l_run, int seq_start,
-                                  int S, int seq, int head, int q_pos, int hl) {
-  const uint32_t ostride_b = p.o_stride_b;
+// half-wave, g = 2gp+1 in the high one.  stage_rows writes the 32 fp16 rows into 8 KiB of a free
+// V buffer (row-major 256 B rows, 16 B chunk c of row r at c ^ (r & 15): conflict-free both
+// ways); flush_rows reads them back four whole rows per instruction and stores them into O and
+// (for the sequence's last row) o_last, so every store writes whole cache lines instead of 32 B
+// pieces of 32 rows.  Exactly kStoreOps<LAST> buffer stores per lane; rows past the sequence (and
+// every row but the last, for o_last) get an offset beyond the buffer resource, so their stores
+// are dropped (S * o stride < 2^31 is validated on the host).
+typedef __attribute__((address_space(3))) char lds_char_t;
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) u4 lds_u4_t;
+__device__ inline lds_char_t* row_stage(lds_char_t* v0, lds_char_t* v1) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  return (wave < 2 ? v0 : v1) + (wave & 1) * (kWaveQ * kRowBytes);
+}
+__device__ inline void stage_rows(const f16x (&o)[4], float l_run, lds_char_t* stage) {
+  int lane = threadIdx.x & 63;
+  asm volatile("" : "+v"(lane));  // the LDS addresses below are computed here, not hoisted
+  const int lq = lane & 31, hl = lane >> 5;
   const float l_tot = pair_sum(l_run);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  const auto ors = make_rsrc(reinterpret_cast<const char*>(p.o) + (uint64_t)seq_start * ostride_b + head * kRowBytes,
-                             (uint32_t)S * ostride_b);
-  const auto lrs = make_rsrc(p.o_last + (int64_t)seq * (kQHeads * kHeadDim) + head * kHeadDim,
-                             p.o_last ? kRowBytes : 0u);
-  const uint32_t orow = (q_pos < S ? (uint32_t)q_pos * ostride_b : 0x80000000u) + 16u * hl;
-  const uint32_t lrow = (q_pos == S - 1 ? 0u : 0x80000000u) + 16u * hl;
-  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 #pragma unroll
   for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -138,11 +142,27 @@ __device__ inline void store_rows(const AttnParams& p, const f16x (&o)[4], float
       const uint32_t b0 = pack2(v[gb] * inv, v[gb + 1] * inv), b1 = pack2(v[gb + 2] * inv, v[gb + 3] * inv);
       const auto r0 = __builtin_amdgcn_permlane32_swap(a0, b0, false, false);
       const auto r1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
-      const u4 val = {r0[0], r1[0], r0[1], r1[1]};
-      const uint32_t d = 2u * (32 * db + 16 * gp);  // + 16 hl, already in orow / lrow
-      if (LAST) __builtin_amdgcn_raw_buffer_store_b128(val, lrs, lrow + d, 0, 0);
-      __builtin_amdgcn_raw_buffer_store_b128(val, ors, orow + d, 0, 0);
+      const int cw = 4 * db + 2 * gp + hl;  // 16 B chunk of row lq
+      *(lds_u4_t*)(stage + lq * kRowBytes + ((cw ^ (lq & 15)) << 4)) = u4{r0[0], r1[0], r0[1], r1[1]};
     }
+}
+template <bool LAST>
+__device__ inline void flush_rows(const AttnParams& p, int seq_start, int S, int seq, int head, int q_row0,
+                                  const lds_char_t* stage) {
+  int lane = threadIdx.x & 63;
+  asm volatile("" : "+v"(lane));
+  const uint32_t ostride_b = p.o_stride_b;
+  const auto ors = make_rsrc(reinterpret_cast<const char*>(p.o) + (uint64_t)seq_start * ostride_b + head * kRowBytes,
+                             (uint32_t)S * ostride_b);
+  const auto lrs = make_rsrc(p.o_last + (int64_t)seq * (kQHeads * kHeadDim) + head * kHeadDim,
+                             p.o_last ? kRowBytes : 0u);
+#pragma unroll
+  for (int j = 0; j < kWaveQ / 4; ++j) {
+    const int row = 4 * j + (lane >> 4), cr = lane & 15, q = q_row0 + row;
+    const u4 val = *(const lds_u4_t*)(stage + row * kRowBytes + ((cr ^ (row & 15)) << 4));
+    if (LAST) __builtin_amdgcn_raw_buffer_store_b128(val, lrs, (q == S - 1 ? 0u : 0x80000000u) + 16u * cr, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(val, ors, (q < S ? (uint32_t)q * ostride_b : 0x80000000u) + 16u * cr, 0, 0);
+  }
 }
 
 // SPLIT: the plan has split items (partial-result path compiled in).  LAST: the run writes
@@ -562,19 +582,21 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
       if (it + 1 < ntiles) body(I0{}, it + 1, sA, sB, pA, pB, true, next_index);
     }
     // Hand-over: the next entry's Q, K(0), K(1) (issued with this entry's last tile) have landed
-    // and every wave is past this entry's LDS reads.  This entry's output rows are normalised
-    // and stored first, then the next S(0) goes to the matrix cores: O and the next scores are
-    // never live together (the other workgroup's wavefronts keep the matrix cores busy
-    // meanwhile).  The next entry's first wait allows for these stores still being in flight.
-    if (wi + 1 < i_end) {
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-    }
-    if (!SPLIT || cur.split < 0)
-      store_rows<LAST>(p, o, l_run, seq_start, S, seq, kvh * kGroup + head_in_group, q_pos, hl);
+    // and every wave is past this entry's LDS reads, so the V buffers are free.  This entry's
+    // output rows are normalised into them first, then the next S(0) goes to the matrix cores
+    // (O and the next scores are never live together) and the rows are stored from LDS while
+    // its MFMAs run.  The next entry's first barrier comes after these LDS reads; its first wait
+    // allows for the stores still being in flight.
+    if (wi + 1 < i_end) __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    const bool rows = !SPLIT || cur.split < 0;
+    lds_char_t* const stage = row_stage((lds_char_t*)sV0, (lds_char_t*)sV1);
+    if (rows)
+      stage_rows(o, l_run, stage);
     else
       write_partial(cur);
     if (wi + 1 < i_end) qk(sK0, sA, no_hook);
+    if (rows) flush_rows<LAST>(p, seq_start, S, seq, kvh * kGroup + head_in_group, wq0, stage);
   }
   // The last item's unused prefetch (LDS-DMA included) lands before the workgroup leaves.
   __builtin_amdgcn_s_waitcnt(0);
@@ -584,8 +606,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
 // redoes wavefront w's output rows of item i: thread 64 db + lane combines dims 32db..32db+31 of
 // lane's row -- records 2db and 2db+1 of every chunk -- in chunk order: m = max_c m_c,
 // w_c = 2^(m_c - m) l_c, O = sum_c w_c (O/l)_c / sum_c w_c (a chunk with no key for the row has
-// m_c = -inf and weighs 0).  All of a thread's loads issue at once; store_rows' layout applies
-// per 32-dim block.  The fp16 halves are taken apart with integer shifts: hipcc has compiled the
+// m_c = -inf and weighs 0).  All of a thread's loads issue at once; stores go row-per-lane as the
+// attention kernel's registers hold them, per 32-dim block.  The fp16 halves are taken apart with integer shifts: hipcc has compiled the
 // element reads of a packed fp16 vector in an unrolled loop as element 0.
 constexpr int kMergeMaxChunks = 8;  // chunks merged per pass (more are folded in further passes)
 __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnParams p) {
@@ -636,7 +658,7 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnParams p) {
     }
     m = mp;
   }
-  // Output: the block of dims 32db..32db+31 of this wave's rows, as store_rows lays them out.
+  // Output: the block of dims 32db..32db+31 of this wave's rows (lanes l and l^32: row l % 32).
   const float inv = l > 0.f ? 1.f / l : 0.f;  // l: the chunks' whole-row sums
   const int S = w.seq_len, head = (w.seq_kvh & 15) * kGroup + (wave >> 1);
   const int q_pos = w.q_block * kBlockQ + (wave & 1) * kWaveQ + lq;
