@@ -24,7 +24,9 @@
 //   * no per-tile row max: probabilities are taken against the entry's first-tile row max and
 //     O and l are rescaled only when a later tile's probabilities could leave fp16 range;
 //   * causal and prefix/local masks skip whole key tiles (key_tiles); element masks run only on
-//     tiles that straddle a boundary (tile_full).
+//     tiles that straddle a boundary (tile_full);
+//   * output rows go through LDS and leave as whole 128-byte lines, non-temporal, so the L2
+//     keeps the K/V tiles that later items of the same sequence re-read.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -55,9 +57,9 @@ constexpr float kLazyLimit = 32768.f;
 constexpr int kPartialRecords = 9;
 
 // Vector-memory instructions per lane that one item's prologue loads (Q: 8 x 16 B, K tiles 0
-// and 1: kLoadsPerTile each) and that one item's epilogue stores (O rows, 8 x 16 B, plus as many
-// for the o_last row when the run has one; always issued: out-of-range lanes are dropped by the
-// buffer resource).  The s_waitcnt counts below rely on these being exact; vector memory
+// and 1: kLoadsPerTile each) and that one item's epilogue stores (O rows, 8 x 16 B per lane, plus
+// as many for the o_last row when the run has one; always issued: out-of-range rows are dropped
+// by the buffer resource).  The s_waitcnt counts below rely on these being exact; vector memory
 // operations retire in issue order.
 constexpr int kPrefetchOps = 8 + 2 * kLoadsPerTile;
 template <bool LAST>
