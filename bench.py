@@ -27,6 +27,7 @@ import hashlib
 import importlib.util
 import json
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -473,12 +474,15 @@ def model_timing(reps, names=("full", "sparse", "cfg4", "cfg1", "cfg3")):
 
 
 def kernel_sources_sha():
-    """Hash of the sources the attention launch is built from (kernels and planner): HBM traffic
-    measured on other sources (profiles/traffic.json) is not reported as this build's."""
+    """Hash of the code the attention launch is built from (kernels and planner, with comments
+    and whitespace removed): HBM traffic measured on other code (profiles/traffic.json) is not
+    reported as this build's."""
     h = hashlib.sha256()
     for f in ("attn_fwd.hip", "attn_common.h", "planner.h", "planner.cpp"):
-        with open(os.path.join(PKG, "csrc", f), "rb") as fh:
-            h.update(fh.read())
+        with open(os.path.join(PKG, "csrc", f), encoding="utf-8") as fh:
+            text = re.sub(r"/\*.*?\*/", " ", fh.read(), flags=re.S)
+        text = re.sub(r"//[^\n]*", " ", text)
+        h.update(" ".join(text.split()).encode())
     return h.hexdigest()[:16]
 
 
