@@ -49,8 +49,10 @@ extern "C" {
 /* 4: qattn_qk_norm_rope_qkv, qattn_run_update; qattn_qk_norm_rope takes heads in multiples of 4
  * 5: the model forward: qattn_embed_q6k, qattn_rmsnorm, qattn_swiglu, qattn_model_*,
  *    qattn_model_plan_*
- * 6: qattn_q4_matmul_swiglu; the model plan's FFN gate/up projection and SwiGLU are one launch */
-#define QATTN_ABI_VERSION 6
+ * 6: qattn_q4_matmul_swiglu; the model plan's FFN gate/up projection and SwiGLU are one launch
+ * 7: qattn_run_update no longer waits for the device (two work-list images per run);
+ *    qattn_debug_fail_allocs */
+#define QATTN_ABI_VERSION 7
 
 #define QATTN_Q_HEADS 16
 #define QATTN_KV_HEADS 8
@@ -135,7 +137,10 @@ enum qattn_run_flags {
  * QATTN_FLAG_BATCH_INVARIANT, uploads it) and returns a run that owns its device work list and
  * split-K workspace. */
 int qattn_run_create(qattn_ctx* ctx, const qattn_run_desc* desc, qattn_run** out);
-/* Enqueues the attention kernel of a run on `stream` (NULL: the context stream). */
+/* Enqueues the attention kernel of a run on `stream` (NULL: the context stream), followed by the
+ * split-K merge kernel when the plan splits items.  Launches of one run must not overlap on the
+ * device (one stream, or streams the caller orders): a split plan's launches share the run's
+ * partial-result workspace. */
 int qattn_run_encode(qattn_run* run, qattn_stream_t stream);
 /* Re-points a run at other tensors of the same shape (layers sharing one packing). */
 int qattn_run_rebind(qattn_run* run, const void* q, const void* k, const void* v, void* o,
@@ -144,9 +149,15 @@ int qattn_run_rebind(qattn_run* run, const void* q, const void* k, const void* v
  * (validated as by qattn_run_create).  The reference creates a run per (batch, sequence) plan
  * shape and rebuilds its uniforms per batch (embedding-engine.ts:70-75, ops.ts:327-343); a
  * varlen batch changes the work list, so one run kept at capacity takes every batch of a plan.
- * Waits for the device to be idle (launches of the previous plan may still read its work list),
- * uploads the new work list, and allocates device memory only when the work list or the split
- * workspace outgrows every earlier one.  The tensors must hold the new token count. */
+ * The run keeps two work-list images: the new plan is uploaded (synchronously) into the one the
+ * installed plan does not use, after waiting only for the earlier launches of this run that read
+ * that image -- never for the device or other streams -- and the run switches to it once the
+ * upload succeeded.  To know when those launches end, the update records an event on each stream
+ * the installed plan was encoded on: those streams must still exist when the run is updated or
+ * destroyed.  Device memory is allocated only when the work list or the split workspace
+ * outgrows every earlier one (and hipFree of the outgrown buffer may then wait for the device).
+ * On failure the run keeps its previous plan, intact and usable.  The tensors must hold the new
+ * token count. */
 int qattn_run_update(qattn_run* run, const int32_t* cu_seqlens, int32_t nseq);
 void qattn_run_destroy(qattn_run* run);
 
@@ -211,6 +222,12 @@ int qattn_debug_xcd_map(qattn_ctx* ctx, int32_t n, int32_t* host_out);
 int qattn_debug_mask(qattn_ctx* ctx, int32_t L, int32_t mask, int32_t prefix, int32_t window,
                      uint32_t* host_bits);
 
+/* Failure injection, no counterpart in the reference: the next n device allocations that
+ * qattn_run_create / qattn_run_update make for a work list or split workspace fail as if the
+ * device were out of memory (QATTN_ENOMEM).  n = 0 cancels.  Lets tests drive the error paths
+ * of a re-plan; process-wide, not for production use. */
+void qattn_debug_fail_allocs(int32_t n);
+
 /* Host evaluation of the same iteration code (attn_common.h is compiled for host and device):
  * no device needed.  Same output layout as qattn_debug_mask. */
 int qattn_plan_mask(int32_t L, int32_t mask, int32_t prefix, int32_t window, uint32_t* host_bits);
@@ -220,7 +237,8 @@ int qattn_plan_mask(int32_t L, int32_t mask, int32_t prefix, int32_t window, uin
  * that also records, for every query head h, packed row t and key k of t's sequence, bit k%32
  * of word host_bits[(h*T + t)*W + k/32] iff the masked score it computed for (t, k) is finite
  * (T = tokens, W = *words_per_row = ceil(longest sequence / 32)).  The run's output buffers are
- * written as by qattn_run_encode (o_last excepted).  host_bits NULL: only *words_per_row.
+ * written as by qattn_run_encode (split plans: the merge kernel runs too; o_last excepted).
+ * host_bits NULL: only *words_per_row.
  * Allocates a device buffer and synchronizes; a diagnostic, not for the hot path. */
 int qattn_debug_run_mask(qattn_run* run, uint32_t* host_bits, int64_t capacity_words,
                          int32_t* words_per_row);

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -52,15 +53,27 @@ constexpr size_t kScratchBytes = (size_t)1 << 20;
 }
 static __device__ __align__(256) char scratch[kScratchBytes];
 
+// A run keeps two plan images (work list, split items' chunk-0 entries, slot offsets) so that a
+// re-plan never writes the image a launch may still be reading: the installed plan lives in
+// image `cur`, a re-plan fills image cur ^ 1 and then switches.  An encode only notes its stream
+// in `streams[cur]` (no per-launch event: an event record between back-to-back launches costs
+// 2.5-3.5 us each on MI355X).  When a re-plan retires image i it records one event on each of
+// those streams (`fences[i]`), after every launch that read the image; the re-plan that later
+// overwrites image i waits for exactly those events -- in the engine's steady state they completed
+// long before -- instead of for the device.
 struct qattn_run {
   qattn_ctx* ctx = nullptr;
-  AttnParams params{};
-  void* plan_dev = nullptr;   // the plan image (work list, tile list, slot offsets)
-  void* split_dev = nullptr;  // the chunks' partial results (merged by a second kernel)
-  size_t plan_capacity = 0;   // bytes at plan_dev
+  AttnParams params{};         // launch arguments of the installed plan (image `cur`)
+  void* plan_dev[2] = {nullptr, nullptr};
+  size_t plan_capacity[2] = {0, 0};  // bytes at plan_dev[i]
+  std::vector<hipStream_t> streams[2];  // streams that launched image i since it was installed
+  std::vector<hipEvent_t> fences[2];    // recorded on those streams when image i was retired
+  int cur = -1;                // image of the installed plan (-1: none yet)
+  void* split_dev = nullptr;   // the chunks' partial results (merged by a second kernel); one
+                               // workspace: launches of one run are ordered on the device
   int32_t partial_capacity = 0;  // partial-result records at split_dev
-  qattn_run_desc desc{};      // the description it was created with (cu_seqlens: not kept)
-  int32_t max_len = 0;        // longest sequence
+  qattn_run_desc desc{};       // the description it was created with (cu_seqlens: not kept)
+  int32_t max_len = 0;         // longest sequence
   qattn_run_info info{};
 };
 
@@ -317,9 +330,50 @@ int qattn_plan_slots(const qattn_run_desc* desc, int32_t max_slots, int32_t* slo
 
 namespace {
 
-// Plans a validated description into `run`: the work list goes to the run's device buffer and
-// the split workspace is sized for it, both reallocated only when they must grow.  The device
-// must not be running a launch of the run's previous plan.
+// qattn_debug_fail_allocs: device allocations of install_plan still to fail.
+std::atomic<int32_t> g_fail_allocs{0};
+hipError_t plan_malloc(void** p, size_t bytes) {
+  int32_t n = g_fail_allocs.load();
+  while (n > 0)
+    if (g_fail_allocs.compare_exchange_weak(n, n - 1)) return hipErrorOutOfMemory;
+  return hipMalloc(p, bytes);
+}
+
+// Records, on every stream that launched image i since it was installed, an event after those
+// launches (fences[i]), and forgets the streams: image i's launches are then covered by its fences.
+hipError_t retire_image(qattn_run* run, int i) {
+  for (hipStream_t s : run->streams[i]) {
+    hipEvent_t ev = nullptr;
+    hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventRecord(ev, s);
+    if (e != hipSuccess) {
+      if (ev) (void)hipEventDestroy(ev);
+      return e;
+    }
+    run->fences[i].push_back(ev);
+  }
+  run->streams[i].clear();
+  return hipSuccess;
+}
+
+// Waits until no launch that reads image i (already retired) is still running.
+hipError_t wait_image(qattn_run* run, int i) {
+  auto& f = run->fences[i];
+  while (!f.empty()) {
+    const hipError_t e = hipEventSynchronize(f.back());
+    if (e != hipSuccess) return e;
+    (void)hipEventDestroy(f.back());
+    f.pop_back();
+  }
+  return hipSuccess;
+}
+
+// Plans a validated description into `run` as one transaction: the new plan image goes to the
+// image slot the installed plan does not use (after the launches that last read that slot have
+// finished), growing it or the split workspace only when they are too small; the run switches to
+// the new plan only once everything has succeeded.  On any failure the installed plan, its
+// launch arguments and every buffer they point to stay as they were, so later encodes stay valid.
+// The only device-wide wait left is hipFree's, and only when a buffer must grow.
 int install_plan(qattn_run* run, const qattn_run_desc* d) {
   qattn_ctx* ctx = run->ctx;
   Plan plan;
@@ -336,28 +390,42 @@ int install_plan(qattn_run* run, const qattn_run_desc* d) {
   if (heads_bytes) std::memcpy(image.data() + items_bytes, plan.split_heads.data(), heads_bytes);
   std::memcpy(image.data() + items_bytes + heads_bytes, plan.slot_begin.data(), slots_bytes);
   DeviceGuard g(ctx->device);
-  if (image.size() > run->plan_capacity) {
-    if (run->plan_dev) (void)hipFree(run->plan_dev);
-    run->plan_dev = nullptr;
-    run->plan_capacity = 0;
-    hipError_t e = hipMalloc(&run->plan_dev, image.size());
+  const int next = run->cur < 0 ? 0 : run->cur ^ 1;
+  // Fences for the installed plan's launches so far (waited on by the re-plan after this one);
+  // extra fences from an update that fails later are harmless.
+  if (run->cur >= 0) HIP_TRY(ctx, retire_image(run, run->cur));
+  HIP_TRY(ctx, wait_image(run, next));
+  if (image.size() > run->plan_capacity[next]) {
+    void* grown = nullptr;
+    hipError_t e = plan_malloc(&grown, image.size());
     if (e != hipSuccess) return fail(ctx, QATTN_ENOMEM, "hipMalloc(work list): %s", hipGetErrorString(e));
-    run->plan_capacity = image.size();
+    if (run->plan_dev[next]) (void)hipFree(run->plan_dev[next]);  // unused: waited for above
+    run->plan_dev[next] = grown;
+    run->plan_capacity[next] = image.size();
   }
-  hipError_t e = hipMemcpy(run->plan_dev, image.data(), image.size(), hipMemcpyHostToDevice);
-  if (e != hipSuccess) return fail(ctx, QATTN_EHIP, "hipMemcpy(work list): %s", hipGetErrorString(e));
   if (plan.partials > run->partial_capacity) {
-    if (run->split_dev) (void)hipFree(run->split_dev);
-    run->split_dev = nullptr;
-    run->partial_capacity = 0;
-    e = hipMalloc(&run->split_dev, (size_t)plan.partials * kPartialBytes);
+    // The installed plan may have launches in flight on this workspace: wait for them, then move
+    // it to a larger one, which serves the installed plan as well as the new one.
+    if (run->cur >= 0) HIP_TRY(ctx, wait_image(run, run->cur));
+    void* grown = nullptr;
+    hipError_t e = plan_malloc(&grown, (size_t)plan.partials * kPartialBytes);
     if (e != hipSuccess)
       return fail(ctx, QATTN_ENOMEM, "split workspace (%d chunks): %s", plan.partials, hipGetErrorString(e));
+    if (run->split_dev) (void)hipFree(run->split_dev);
+    run->split_dev = grown;
     run->partial_capacity = plan.partials;
+    run->params.partials = static_cast<float*>(grown);
   }
-  fill_params(&run->params, d, mask, info.slots, run->plan_dev, items_bytes, heads_bytes);
-  run->params.partials = static_cast<float*>(run->split_dev);
-  run->params.n_splits = plan.splits;
+  // Synchronous from pageable host memory: the image is on the device when this returns, and
+  // the copy waits for nothing else on the device.
+  HIP_TRY(ctx, hipMemcpy(run->plan_dev[next], image.data(), image.size(), hipMemcpyHostToDevice));
+  // Commit.
+  AttnParams p{};
+  fill_params(&p, d, mask, info.slots, run->plan_dev[next], items_bytes, heads_bytes);
+  p.partials = static_cast<float*>(run->split_dev);
+  p.n_splits = plan.splits;
+  run->params = p;
+  run->cur = next;
   run->info = info;
   run->max_len = 0;
   for (int32_t s = 0; s < d->nseq; ++s) run->max_len = std::max(run->max_len, d->cu_seqlens[s + 1] - d->cu_seqlens[s]);
@@ -367,13 +435,27 @@ int install_plan(qattn_run* run, const qattn_run_desc* d) {
   return QATTN_OK;
 }
 
+// Enqueues `p` (the run's launch arguments, or a variant of them) on `stream` and notes the
+// stream as one that reads image `cur` (a fence goes there when the image is retired).
+int launch_run(qattn_run* run, const AttnParams& p, hipStream_t stream, bool merge) {
+  qattn_ctx* ctx = run->ctx;
+  auto& used = run->streams[run->cur];
+  if (std::find(used.begin(), used.end(), stream) == used.end()) used.push_back(stream);
+  HIP_TRY(ctx, launch_attn_fwd(p, stream));
+  if (merge) HIP_TRY(ctx, launch_attn_merge(p, stream));
+  return QATTN_OK;
+}
+
 void free_run(qattn_run* run) {
-  if (run->plan_dev || run->split_dev) {
-    DeviceGuard g(run->ctx->device);
-    (void)hipStreamSynchronize(run->ctx->stream);
-    if (run->plan_dev) (void)hipFree(run->plan_dev);
-    if (run->split_dev) (void)hipFree(run->split_dev);
+  DeviceGuard g(run->ctx->device);
+  for (int i = 0; i < 2; ++i) {
+    if (retire_image(run, i) != hipSuccess)
+      for (hipStream_t s : run->streams[i]) (void)hipStreamSynchronize(s);
+    (void)wait_image(run, i);
   }
+  for (int i = 0; i < 2; ++i)
+    if (run->plan_dev[i]) (void)hipFree(run->plan_dev[i]);
+  if (run->split_dev) (void)hipFree(run->split_dev);
   delete run;
 }
 
@@ -405,11 +487,6 @@ int qattn_run_update(qattn_run* run, const int32_t* cu_seqlens, int32_t nseq) {
   d.nseq = nseq;
   int rc = validate_desc(run->ctx, &d);
   if (rc) return rc;
-  {
-    // Launches of the previous plan (on any stream) may still read its work list.
-    DeviceGuard g(run->ctx->device);
-    HIP_TRY(run->ctx, hipDeviceSynchronize());
-  }
   return install_plan(run, &d);
 }
 
@@ -417,9 +494,7 @@ int qattn_run_encode(qattn_run* run, qattn_stream_t stream) {
   if (!run) return fail(nullptr, QATTN_EINVAL, "run is NULL");
   qattn_ctx* ctx = run->ctx;
   DeviceGuard g(ctx->device);
-  HIP_TRY(ctx, launch_attn_fwd(run->params, pick_stream(ctx, stream)));
-  HIP_TRY(ctx, launch_attn_merge(run->params, pick_stream(ctx, stream)));
-  return QATTN_OK;
+  return launch_run(run, run->params, pick_stream(ctx, stream), true);
 }
 
 int qattn_run_rebind(qattn_run* run, const void* q, const void* k, const void* v, void* o,
@@ -563,14 +638,20 @@ int qattn_debug_run_mask(qattn_run* run, uint32_t* host_bits, int64_t capacity_w
   p.maskbits = dev;
   p.mask_rows = (int32_t)T;
   p.mask_words = words;
+  // The attention kernel's mask variant, then (split plans) the merge kernel, so the output rows
+  // are written as by qattn_run_encode.
   hipError_t e = hipMemsetAsync(dev, 0, (size_t)need * sizeof(uint32_t), ctx->stream);
-  if (e == hipSuccess) e = launch_attn_fwd(p, ctx->stream);
-  if (e == hipSuccess) e = hipMemcpyAsync(host_bits, dev, (size_t)need * sizeof(uint32_t), hipMemcpyDeviceToHost, ctx->stream);
-  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  int rc = e == hipSuccess ? launch_run(run, p, ctx->stream, true) : QATTN_OK;
+  if (e == hipSuccess && rc == QATTN_OK)
+    e = hipMemcpyAsync(host_bits, dev, (size_t)need * sizeof(uint32_t), hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess && rc == QATTN_OK) e = hipStreamSynchronize(ctx->stream);
   (void)hipFree(dev);
+  if (rc != QATTN_OK) return rc;
   if (e != hipSuccess) return fail(ctx, QATTN_EHIP, "run mask: %s", hipGetErrorString(e));
   return QATTN_OK;
 }
+
+void qattn_debug_fail_allocs(int32_t n) { g_fail_allocs.store(n > 0 ? n : 0); }
 
 int qattn_plan_mask(int32_t L, int32_t mask, int32_t prefix, int32_t window, uint32_t* host_bits) {
   if (L < 0 || L > (1 << 20)) return fail(nullptr, QATTN_EINVAL, "L=%d outside [0, 2^20]", L);

@@ -131,6 +131,7 @@ def lib():
         "qattn_debug_mask": (ctypes.c_int, [vp, i32, i32, i32, i32, vp]),
         "qattn_plan_mask": (ctypes.c_int, [i32, i32, i32, i32, vp]),
         "qattn_debug_run_mask": (ctypes.c_int, [vp, vp, i64, ctypes.POINTER(i32)]),
+        "qattn_debug_fail_allocs": (None, [i32]),
         "qattn_qk_norm_rope": (ctypes.c_int, [vp, vp, i64, i64, i32, vp, i32, vp,
                                               ctypes.c_double, ctypes.c_double, vp]),
         "qattn_qk_norm_rope_qkv": (ctypes.c_int, [vp, vp, i64, vp, i64, vp, i64, vp, i32, vp, vp,

@@ -148,6 +148,27 @@ def test_model_forward_matches_oracle(ctx, weights, dmodel, lengths):
     print(f"lengths {lengths}: max|err| {e:.3e}, min cos {c:.7f}")
 
 
+@pytest.mark.timeout(400)
+def test_model_forward_28_layers_matches_oracle(ctx):
+    """The model's real depth (LAYERS = 28, model.ts:21, 91-104): fp16 activations between the
+    nine stages of every layer must not drift past the bar over 28 layers.  A mixed packing with
+    a sequence longer than prefix + window (the sparse mask's long-range rows) and a short one."""
+    weights = mr.synthetic_weights(28, 28, vocab=300)
+    m = DeviceModel(ctx, weights)
+    try:
+        lengths = [5, 64, 200, 700]
+        rng = np.random.default_rng(28)
+        cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+        ids = rng.integers(0, weights["vocab"], int(cu[-1])).astype(np.int32)
+        print(f"28-layer forward {lengths}", flush=True)
+        got = _run(ctx, m, ids, cu)
+        want = mr.forward(weights, ids, cu)
+        e, c = _check_embeddings(got, want)
+        print(f"28 layers, lengths {lengths}: max|err| {e:.3e}, min cos {c:.7f}", flush=True)
+    finally:
+        m.free()
+
+
 def test_model_plan_reuse_and_rejects(ctx, qattn, weights, dmodel):
     rng = np.random.default_rng(9)
     plan = dmodel.model.plan(400, 4)

@@ -302,6 +302,22 @@ def _exact_and_gpu(ctx, qattn, oracle, lengths, config=0, mask=1, P=176, W=432, 
     return case, (q, k, v, cu), got, exact
 
 
+@pytest.mark.timeout(300)
+@pytest.mark.parametrize("label,config,lengths,mask", [("16x500 full causal", 2, [500] * 16, 0),
+                                                       ("1x5000 sparse", 5, [5000], 1)])
+def test_benched_launch_every_row(ctx, qattn, oracle, label, config, lengths, mask):
+    """The two launches bench.py times -- same seeds (layer 0), mask kind, default flags (split-K
+    allowed), no o_last -- compared with the f64 oracle on every row and every query head, so the
+    headline numbers are measured on output that is checked in full, split items included."""
+    print(f"benched launch {label}: all rows", flush=True)
+    case, _, got, exact = _exact_and_gpu(ctx, qattn, oracle, lengths, config=config, mask=mask)
+    info = ctx.run(case.desc).info()
+    if mask == 1:
+        assert info.split_items > 0  # the split-K path (chunks + merge) is part of this check
+    compare(got, exact, f"{label} (all {case.T} rows, {info.split_items} split items)")
+    case.free()
+
+
 def test_config0_single_50(ctx, qattn, oracle):
     case, (q, k, v, cu), got, exact = _exact_and_gpu(ctx, qattn, oracle, [50])
     compare(got, exact, "cfg0 1x50")
@@ -484,6 +500,72 @@ def test_run_update_replans_in_place(ctx, qattn, oracle, flags):
     run.update(cu_of([500] * 4))  # still usable
     run.destroy()
     for b in (bq, bk, bv, bo, bl):
+        b.free()
+
+
+@pytest.mark.parametrize("flags", [0, 1])
+def test_run_update_while_launches_are_in_flight(ctx, qattn, oracle, flags):
+    """Re-plans queued behind running launches: each batch gets its own tensors (rebind), the run
+    is re-planned and encoded with no synchronisation in between, so every update overwrites a
+    work-list image while earlier launches may still run.  Each batch's output must equal a fresh
+    run's bit for bit (an update that overwrote a work list in use would corrupt an earlier
+    batch)."""
+    batches = [[500] * 16, [5000], [1, 609, 64, 177, 1500, 2], [120] * 40, [3000, 700], [64] * 3]
+    cases = []
+    for i, lengths in enumerate(batches):
+        cu = cu_of(lengths)
+        q, k, v = oracle.gen_qkv(3, i, cu)
+        cases.append(Case(ctx, qattn, q, k, v, cu, flags=flags))
+    run = ctx.run(cases[0].desc)
+    outs = []
+    for c in cases:
+        o = ctx.alloc(c.T * 4096)
+        outs.append(o)
+        run.rebind(c.qbuf.ptr, c.kbuf.ptr, c.vbuf.ptr, o.ptr)
+        run.update(c.cu)
+        run.encode()
+    ctx.synchronize()
+    for c, o, lengths in zip(cases, outs, batches):
+        got = o.read(np.uint16, (c.T, 2048))
+        assert np.array_equal(got, c.run()), lengths
+        o.free()
+        c.free()
+    run.destroy()
+
+
+@pytest.mark.parametrize("flags", [0, 1])
+def test_failed_update_keeps_the_previous_plan(ctx, qattn, oracle, flags):
+    """A re-plan whose device allocation fails (injected: qattn_debug_fail_allocs) returns
+    QATTN_ENOMEM and leaves the run on its previous plan: the next encode computes the previous
+    batch bit for bit; once allocations succeed again the same update goes through."""
+    cap = 5000
+    bq, bk, bv, bo = ctx.alloc(cap * 4096), ctx.alloc(cap * 2048), ctx.alloc(cap * 2048), ctx.alloc(cap * 4096)
+    run = ctx.run(qattn.make_desc(bq.ptr, bk.ptr, bv.ptr, bo.ptr, cu_of([7]), flags=flags))
+    small, big = cu_of([500] * 4), cu_of([5000])
+    q, k, v = oracle.gen_qkv(1, 4, small)
+    bq.write(q)
+    bk.write(k)
+    bv.write(v)
+    run.update(small)  # image 1; image 0 still holds the 7-token plan's small buffer
+    fresh = Case(ctx, qattn, q, k, v, small, flags=flags)
+    want = fresh.run()
+    try:
+        qattn.lib().qattn_debug_fail_allocs(1)
+        with pytest.raises(qattn.QattnError) as e:
+            run.update(big)  # needs a larger work list in image 0: the allocation fails
+        assert e.value.code == qattn.ENOMEM
+    finally:
+        qattn.lib().qattn_debug_fail_allocs(0)
+    assert run.info().tokens == 2000
+    bo.fill_u16(0x7E00)
+    run.encode()
+    ctx.synchronize()
+    assert np.array_equal(bo.read(np.uint16, (2000, 2048)), want)
+    run.update(big)
+    assert run.info().tokens == 5000
+    run.destroy()
+    fresh.free()
+    for b in (bq, bk, bv, bo):
         b.free()
 
 

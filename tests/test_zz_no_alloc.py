@@ -49,11 +49,18 @@ def test_prefill_static_two_calls_second_smaller(ctx, qattn, oracle):
 
 
 def test_prefill_static_rejects_oversized_plan_before_device_work(ctx, qattn):
-    # 40 sequences x 8000 tokens -> 40 * 125 * 8 = 40000 work entries > the static capacity.  The
-    # pointers are never dereferenced: the capacity check precedes every device call.
-    fake = 1 << 32
-    cu = cu_of([8000] * 40)
-    desc = qattn.make_desc(fake, fake, fake, fake, cu, 1, 176, 432)
+    # 5000 one-token sequences -> 5000 x 8 = 40000 work entries (32 bytes each), more than the
+    # 1 MiB static work list holds (checked on the host first).  The tensors are real device
+    # buffers sized for the batch: no attention launch can be handed a wild address.
+    lengths = [1] * 5000
+    cu = cu_of(lengths)
+    T = int(cu[-1])
+    bufs = [ctx.alloc(T * 4096), ctx.alloc(T * 2048), ctx.alloc(T * 2048), ctx.alloc(T * 4096)]
+    desc = qattn.make_desc(*(b.ptr for b in bufs), cu, 1, 176, 432, flags=FLAG_BATCH_INVARIANT)
+    entries, info = qattn.plan_describe(desc)
+    assert len(entries) == 40000 and len(entries) * 32 > (1 << 20)
     with pytest.raises(qattn.QattnError) as e:
         ctx.prefill_static(desc)
     assert e.value.code == qattn.EINVAL and b"static" in qattn.lib().qattn_last_error(ctx.handle)
+    for b in bufs:
+        b.free()
