@@ -7,12 +7,13 @@ of independent seeded Q/K/V resident in HBM:
   * 1 x 5000 tokens, 176-prefix + 432-local sparse causal (the metric's sparse row)
 Every launch is one layer's attention through the C ABI (qattn_run_encode), exactly what the
 Node engine issues.  Timing: HIP events on the launch stream around exactly K steps, with a
-device synchronize on both sides.  A second pass brackets each workload's 28 back-to-back
-layer launches with one pair of events and divides by 28, to get the workload's average launch
-duration (the gaps between consecutive launches included, no event inside the sequence) -- for
-the headline workloads and, reported beside them in config.breakdown, for the other BASELINE
-configs (0: 1 x 50, 1: 16 ragged 10..150, 3: 1 x 1500 sparse, 4: 4 x 5000 sparse with
-last-token rows).
+device synchronize on both sides; roofline.achieved is the step's algorithmic FLOPs over the same
+step time.  A second pass times each workload alone on the same basis -- its 28 layer launches,
+several rounds back to back between one pair of events, no synchronisation inside -- and divides
+by the launch count: the workload's average launch duration (gaps between consecutive launches
+included), for the headline workloads and, reported beside them in config.breakdown, for the
+batch-invariant 1 x 5000 plan the engine uses and the other BASELINE configs (0: 1 x 50, 1: 16
+ragged 10..150, 3: 1 x 1500 sparse, 4: 4 x 5000 sparse with last-token rows).
 
 cpu_baseline: the reference's tiled kernel (src/webgpu/ops.ts:168-241) restated in JavaScript
 (oracle/tiled16.js, f16 rounding points as the WGSL) and run under Node on this host's cores,
@@ -62,18 +63,24 @@ def config1_lengths():
             for i in range(16)]
 
 
+FLAG_BATCH_INVARIANT = 1
 WORKLOADS = {
-    # name: (config id for seeds, lengths, mask kind, o_last, description)
-    "full": (2, [500] * 16, 0, False, "16x500 full causal"),
-    "sparse": (5, [5000], 1, False, "1x5000 sparse (176 prefix + 432 window)"),
-    "cfg0": (0, [50], 1, False, "cfg0 1x50 causal"),
-    "cfg1": (1, None, 1, False, "cfg1 16 ragged 10..150 causal"),
-    "cfg3": (3, [1500], 1, False, "cfg3 1x1500 sparse (176 prefix + 432 window)"),
-    "cfg4": (4, [5000] * 4, 1, True, "cfg4 4x5000 sparse (176 prefix + 432 window) + last rows"),
+    # name: (config id for seeds, lengths, mask kind, o_last, description, run flags)
+    "full": (2, [500] * 16, 0, False, "16x500 full causal", 0),
+    "sparse": (5, [5000], 1, False, "1x5000 sparse (176 prefix + 432 window)", 0),
+    # The same launch with the plan the Node engine and the model plan use by default
+    # (QATTN_FLAG_BATCH_INVARIANT: no split-K, no merge kernel).
+    "sparse_bi": (5, [5000], 1, False, "1x5000 sparse, batch-invariant plan (the engine's default)",
+                  FLAG_BATCH_INVARIANT),
+    "cfg0": (0, [50], 1, False, "cfg0 1x50 causal", 0),
+    "cfg1": (1, None, 1, False, "cfg1 16 ragged 10..150 causal", 0),
+    "cfg3": (3, [1500], 1, False, "cfg3 1x1500 sparse (176 prefix + 432 window)", 0),
+    "cfg4": (4, [5000] * 4, 1, True, "cfg4 4x5000 sparse (176 prefix + 432 window) + last rows", 0),
 }
 SETS = {"both": ["full", "sparse"], "full": ["full"], "sparse": ["sparse"], "cfg3": ["cfg3"],
         "cfg4": ["cfg4"]}
-EXTRA = ["cfg0", "cfg1", "cfg3", "cfg4"]  # reported in the breakdown of the default run
+EXTRA = ["sparse_bi", "cfg0", "cfg1", "cfg3", "cfg4"]  # in the breakdown of the default run
+PEAK_HBM_MEASURED_GBS = 6100.0  # streaming copy on these boxes (the attainable-roofline ceiling)
 
 
 def lengths_of(name):
@@ -98,7 +105,7 @@ class Workload:
 
     def __init__(self, ctx, q, name):
         self.name = name
-        cfg, _, mask, o_last, desc = WORKLOADS[name]
+        cfg, _, mask, o_last, desc, flags = WORKLOADS[name]
         self.desc_text = desc
         self.lengths = lengths_of(name)
         self.cu = np.concatenate([[0], np.cumsum(self.lengths)]).astype(np.int32)
@@ -112,7 +119,7 @@ class Workload:
             bl = ctx.alloc(nseq * 4096) if o_last else None
             ctx.gen_qkv(cfg, layer, self.cu, bq.ptr, bk.ptr, bv.ptr)
             d = q.make_desc(bq.ptr, bk.ptr, bv.ptr, bo.ptr, self.cu, mask=mask,
-                            o_last=bl.ptr if bl else None)
+                            o_last=bl.ptr if bl else None, flags=flags)
             self.runs.append(ctx.run(d))
             self.bufs += [b for b in (bq, bk, bv, bo, bl) if b]
         ctx.synchronize()
@@ -154,7 +161,7 @@ def node_samples(name, per_stratum):
     sequence 0 (all sequences are alike), `per_stratum` heads each; 1 x 5000: every 16th query
     tile, `per_stratum` heads each (heads cost the same).  A run on N threads takes N heads per
     query tile, so its wall time stays near the one-thread run's."""
-    cfg, _, kind, _, _ = WORKLOADS[name]
+    cfg, _, kind = WORKLOADS[name][:3]
     lengths = lengths_of(name)
     L = lengths[0]
     vt = visited_key_tiles(L, kind)
@@ -565,23 +572,23 @@ def main():
     ms_per_step = region_ms / args.steps
     log(f"timed {args.steps} steps: {region_ms:.3f} ms on device events ({host_ms:.3f} ms host)")
 
-    # ---- per-launch durations (separate pass, same launches; the other configs too): each
-    # workload's 28 layer launches back to back between one pair of events, / 28.  (An event pair
-    # around every single launch would add each event's own dispatch, 1-3 us per launch.) ----
+    # ---- per-workload launch durations on the same basis as `value`: each workload's 28 layer
+    # launches, `reps` rounds back to back between one pair of events on the launch stream, with
+    # no synchronisation inside (so no idle gap and no clock ramp between launches), divided by
+    # the launch count.  The headline workloads' figures times 28 should add up to ms_per_step.
     reps = max(3, min(args.steps, 10))
-    per = {w.name: [] for w in wls + extra}
+    per = {}
     ea, eb = ctx.event(), ctx.event()
-    for w in extra:
-        for _ in range(3):
+    for w in wls + extra:
+        for _ in range(2):
             w.encode_all()
-    for _ in range(reps):
-        for w in wls + extra:
-            ctx.synchronize()
-            ea.record()
+        ctx.synchronize()
+        ea.record()
+        for _ in range(reps):
             w.encode_all()
-            eb.record()
-            ctx.synchronize()
-            per[w.name].append(ea.elapsed_ms(eb) / len(w.runs))
+        eb.record()
+        ctx.synchronize()
+        per[w.name] = ea.elapsed_ms(eb) / (reps * len(w.runs))
     ea.destroy()
     eb.destroy()
 
@@ -589,10 +596,12 @@ def main():
     value = tokens_per_step / (ms_per_step / 1e3)
     total_flops = sum(w.info.flops for w in wls) * LAYERS
     total_bytes = sum(w.info.bytes for w in wls) * LAYERS
-    kern_ms_step = sum(np.mean(per[w.name]) * LAYERS for w in wls)
+    kern_ms_step = sum(per[w.name] * LAYERS for w in wls)
     breakdown = {}
     for w in wls + extra:
-        avg = float(np.mean(per[w.name]))
+        avg = per[w.name]
+        ai = w.info.flops / w.info.bytes
+        attainable = min(PEAK_FP16_TFLOPS * 1e12, ai * PEAK_HBM_MEASURED_GBS * 1e9)
         breakdown[w.name] = {
             "workload": w.desc_text,
             "headline": w in wls,
@@ -602,9 +611,14 @@ def main():
             "mfma_frac": round(w.info.flops / (avg / 1e3) / 1e12 / PEAK_FP16_TFLOPS, 4),
             "gbs": round(w.info.bytes / (avg / 1e3) / 1e9, 1),
             "hbm_frac": round(w.info.bytes / (avg / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
+            "attainable_frac": round(w.info.flops / (avg / 1e3) / attainable, 4),
+            "split_items": w.info.split_items,
         }
         log(f"{w.name}: kernel avg {avg * 1e3:.2f} us, {breakdown[w.name]}")
-    achieved = total_flops / (kern_ms_step / 1e3) / 1e12
+    # The roofline figure on value's own basis: the step's algorithmic FLOPs over the step time.
+    achieved = total_flops / (ms_per_step / 1e3) / 1e12
+    log(f"basis check: headline launches {kern_ms_step:.4f} ms per step back to back vs the step's "
+        f"{ms_per_step:.4f} ms")
 
     traffic, traffic_note = None, "no profiles/traffic.json"
     tpath = os.path.join(REPO, "profiles", "traffic.json")
@@ -658,6 +672,8 @@ def main():
             "peak": PEAK_FP16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
+            "basis": "the step: algorithmic FLOPs of the step's 56 launches / ms_per_step (as value)",
+            "launches_ms_per_step": round(kern_ms_step, 4),
             "traffic": traffic,
             "traffic_note": traffic_note,
             "kernel": "attn_fwd_kernel (+ attn_merge_kernel on split-K plans)",

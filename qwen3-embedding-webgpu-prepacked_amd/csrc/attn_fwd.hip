@@ -227,7 +227,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     // The add stays here (not hoisted into four loop-invariant registers).
     uint32_t step = (uint32_t)(16 * j) * stride_b;
     asm volatile("" : "+s"(step));
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(dst + j * 4096 + wave * 1024), 16, off + step, 0, 0, 0);
+    // The destination (M0) is formed here from one per-wave offset, not kept in 16 registers.
+    uint32_t wbase = (uint32_t)wave * 1024u;
+    asm volatile("" : "+s"(wbase));
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(dst + j * 4096 + wbase), 16, off + step, 0, 0, 0);
   };
   auto load_tile = [&](char* dst, const char* base, uint32_t stride_b, uint32_t off, int kt, int S) {
     const auto rs = tile_rsrc(base, stride_b, kt, S);
