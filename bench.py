@@ -383,7 +383,7 @@ def q4_timing(reps):
     ctx.close()
 
 
-def synthetic_model(ctx, q, n_layers, vocab, seed=0, scale=0.005):
+def synthetic_model(ctx, q, n_layers, vocab, seed=0, scale=0.005, flags=0):
     """Random weights of the model's shapes, written straight into the device layouts the forward
     reads (no file, no packing step): a Q6_K token table of `vocab` rows (random codes, int8
     scales 1..15 with random sign, d ~ 0.006), norm gains 1 + 0.1 N(0,1), and per layer the four
@@ -413,7 +413,7 @@ def synthetic_model(ctx, q, n_layers, vocab, seed=0, scale=0.005):
     layers = [{"attn_norm": gain(1024), "attn_qkv": compact(1024, 4096), "attn_q_norm": gain(128),
                "attn_k_norm": gain(128), "attn_output": compact(2048, 1024), "ffn_norm": gain(1024),
                "ffn_gate_up": compact(1024, 6144), "ffn_down": compact(3072, 1024)} for _ in range(n_layers)]
-    model = ctx.model((table.ptr, blocks.nbytes), gain(1024), layers)
+    model = ctx.model((table.ptr, blocks.nbytes), gain(1024), layers, flags=flags)
     return model, bufs
 
 
@@ -480,6 +480,61 @@ def model_timing(reps, names=("full", "sparse", "cfg4", "cfg1", "cfg3")):
     ctx.close()
 
 
+MATRIX_LENGTHS = (15, 50, 150, 500, 1500, 5000)
+
+
+def model_matrix(reps):
+    """The reference's measurement matrix (README.md:14-21, protocol src/main.ts:302-321) on the
+    28-layer forward: one request and 16 concurrent requests of 15, 50, 150, 500, 1,500 and 5,000
+    tokens, each 16-request round one packed batch (5,000 tokens: four batches of four, as the
+    reference runs it), with the batch-invariant plan the engine uses and the model's 176 + 432
+    mask (full causal up to 608 tokens).  Synthetic weights of the real shapes, random token ids;
+    `reps` forwards between HIP events after 2 warm-ups, then one profiled run for the stage split.
+    Device time only: no tokenizer, no host round trip per request."""
+    q = load_binding()
+    ctx = q.Context(0)
+    model, bufs = synthetic_model(ctx, q, LAYERS, MODEL_VOCAB, flags=FLAG_BATCH_INVARIANT)
+    rng = np.random.default_rng(2)
+    gemm_flop_per_token = 2.0 * (1024 * 4096 + 2048 * 1024 + 1024 * 6144 + 3072 * 1024) * LAYERS
+    plan = model.plan(16 * 1500, 16)  # the largest batch: 16 x 1,500 tokens
+    out = ctx.alloc(16 * 1024 * 4)
+    e0, e1 = ctx.event(), ctx.event()
+    for L in MATRIX_LENGTHS:
+        for conc in (1, 16):
+            per_batch = 4 if (L == 5000 and conc == 16) else conc
+            batches = conc // per_batch
+            lengths = [L] * per_batch
+            cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+            T = int(cu[-1])
+            ids = rng.integers(0, MODEL_VOCAB, T).astype(np.int32)
+            for _ in range(2):
+                plan.run(ids, cu, out.ptr)
+            ctx.synchronize()
+            e0.record()
+            for _ in range(reps * batches):
+                plan.run(ids, cu, out.ptr)
+            e1.record()
+            ctx.synchronize()
+            ms_round = e0.elapsed_ms(e1) / reps  # one round of `conc` requests
+            stages = plan.profile(ids, cu, out.ptr)
+            flop = batches * (gemm_flop_per_token * T + 8192.0 * sum(retained_pairs_sparse(x) for x in lengths) * LAYERS)
+            print(json.dumps({"path": "qattn_model_plan_run (28 layers)", "tokens": L, "concurrency": conc,
+                              "batches_per_round": batches, "runs": reps, "ms_per_round": round(ms_round, 3),
+                              "requests_per_s": round(conc / (ms_round / 1e3), 1),
+                              "tokens_per_s": round(conc * L / (ms_round / 1e3), 1),
+                              "TFLOP/s": round(flop / (ms_round / 1e3) / 1e12, 1),
+                              "frac_of_fp16_peak": round(flop / (ms_round / 1e3) / 1e12 / PEAK_FP16_TFLOPS, 3),
+                              "stage_ms_one_batch": {k: round(v, 3) for k, v in stages.items()}}), flush=True)
+    e0.destroy()
+    e1.destroy()
+    out.free()
+    plan.destroy()
+    model.destroy()
+    for b in bufs:
+        b.free()
+    ctx.close()
+
+
 def kernel_sources_sha():
     """Hash of the code the attention launch is built from (kernels and planner, with comments
     and whitespace removed): HBM traffic measured on other code (profiles/traffic.json) is not
@@ -513,7 +568,13 @@ def main():
                     help="only time N launches of the fused QK-norm + RoPE producer and exit")
     ap.add_argument("--model", type=int, default=0, metavar="N",
                     help="only time N runs of the whole 28-layer forward (synthetic weights) per config and exit")
+    ap.add_argument("--model-matrix", type=int, default=0, metavar="N",
+                    help="only run the reference's single / 16-request matrix at 15..5000 tokens through "
+                         "the 28-layer forward, N rounds each, and exit")
     args = ap.parse_args()
+    if args.model_matrix:
+        model_matrix(args.model_matrix)
+        return
     if args.model:
         if args.workload == "both":
             model_timing(args.model)

@@ -26,6 +26,9 @@
 //     b % 8) walk the N tiles of one M tile: its X rows stay in that XCD's L2;
 //   * the SWIGLU variant (the FFN's gate/up projection, model.ts:126-127) maps each workgroup's B
 //     rows onto a feature's gate and up rows and writes silu(gate) * up instead of the projection.
+//   * launches of at most kQ4DirectBlocks 32 x 32 output blocks (small M) run q4_direct_kernel
+//     instead: one wavefront per block and per workgroup, no LDS, the same MFMA chain per output
+//     element, so its rows equal the tiled kernel's bit for bit.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -277,6 +280,127 @@ __global__ __launch_bounds__(256, 2) void q4_matmul_kernel(const _Float16* __res
   }
 }
 
+// ---- small launches (at most kQ4DirectBlocks 32 x 32 output blocks): one wavefront per block,
+// one wavefront per workgroup, and no LDS.
+// At small M the tiled kernel's time is its K loop's latency chain -- dequantised weights to
+// LDS, barrier, fragment reads, MFMAs -- about 0.3 us per 32-column K block for every M up to
+// ~1,500, on as few as 8 workgroups.  Here each wavefront loads its own X rows and weight records
+// straight into MFMA fragment registers, kQ4Ahead K blocks ahead, dequantises them with the same
+// code and runs the same MFMA chain: per output element the same operands in the same order
+// (K block by K block, its 16-column step 0 then step 1, from a zero accumulator), so the result
+// is bit for bit the tiled kernel's and a row does not depend on the batch it is in.
+// Lane (l32, hl) holds X row m0 + l32 and weight row n0 + l32, columns 16 s + 8 hl .. +7 of the
+// K block in step s (the tiled kernel's fragment layout).  SWIGLU: two chains, the gate rows
+// n0 + l32 and the up rows n_inter + n0 + l32 of the 32 output features n0 .. n0 + 31.
+// A wavefront is bound by its own dequantisation VALU work (~0.11 us per K block, twice that
+// with SWIGLU's two chains) and its X loads, which touch one cache line per row: one wavefront
+// per workgroup spreads the blocks over as many CUs (measured 2x faster than four per
+// workgroup).  Up to 512 blocks (two per CU) it beats the tiled kernel on all four projection
+// shapes; deeper rings and coalesced X loads staged through LDS measured slower.
+constexpr int kQ4DirectBlocks = 512;
+constexpr int kQ4Ahead = 8;  // K blocks in flight per wavefront (a ring of register stages)
+
+template <bool SWIGLU>
+__global__ __launch_bounds__(64) void q4_direct_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, int K,
+                                                        const uint8_t* __restrict__ w, uint32_t w_bytes, int N,
+                                                        _Float16* __restrict__ y, int64_t ldy, int blocks_m,
+                                                        int blocks_total) {
+  const int lane = threadIdx.x & 63, l32 = lane & 31, hl = lane >> 5;
+  // block g: the M blocks of one N block are consecutive (they share weight records in L2)
+  const int g = blockIdx.x;
+  if (g >= blocks_total) return;
+  const int m0 = (g % blocks_m) * 32, n0 = (g / blocks_m) * 32;
+  const int kblocks = K >> 5;
+  const int n_out = SWIGLU ? N >> 1 : N;  // output columns
+
+  const auto xrs = q4_rsrc(x, (uint32_t)M * (uint32_t)ldx * 2u);  // rows >= M read as zeros
+  const auto wrs = q4_rsrc(w, w_bytes);                          // rows >= N read as zeros
+  const auto yrs = q4_rsrc(y, (uint32_t)M * (uint32_t)ldy * 2u);
+  const uint32_t x_row = (uint32_t)(m0 + l32) * (uint32_t)ldx * 2u + 16u * hl;
+  auto w_rec = [&](int n) { return ((uint32_t)(n >> 5) * (uint32_t)kblocks * 32u + (uint32_t)(n & 31)) * kQ4Record; };
+  const uint32_t wg_rec = w_rec(n0 + l32), wu_rec = SWIGLU ? w_rec(n_out + n0 + l32) : 0u;
+  const uint32_t w_step = 32u * kQ4Record;
+
+  struct Stage {
+    h8 a[2];
+    uint32_t sg, su;
+    u2 qg, qu;
+  };
+  constexpr int kOps = SWIGLU ? 6 : 4;  // vector-memory instructions per K block
+  auto load = [&](Stage& st, int kb) {
+    kb = kb < kblocks ? kb : kblocks - 1;  // past the end: re-read the last block (never used)
+    const uint32_t xo = x_row + (uint32_t)kb * 64u;
+    st.a[0] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(xrs, xo, 0, 0));
+    st.a[1] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(xrs, xo + 32u, 0, 0));
+    const uint32_t go = wg_rec + (uint32_t)kb * w_step;
+    st.sg = __builtin_amdgcn_raw_buffer_load_b32(wrs, go, 0, 0);
+    st.qg = __builtin_amdgcn_raw_buffer_load_b64(wrs, go + 4u + 8u * hl, 0, 0);
+    if constexpr (SWIGLU) {
+      const uint32_t uo = wu_rec + (uint32_t)kb * w_step;
+      st.su = __builtin_amdgcn_raw_buffer_load_b32(wrs, uo, 0, 0);
+      st.qu = __builtin_amdgcn_raw_buffer_load_b64(wrs, uo + 4u + 8u * hl, 0, 0);
+    }
+  };
+  f16x acc_g = {}, acc_u = {};
+  auto mma = [&](const Stage& st) {
+    const _Float16 sg = __builtin_bit_cast(h2, st.sg)[0];
+    const h2 scale_g = {sg, sg};
+    acc_g = q4_mfma(st.a[0], dequant8<false>(st.qg, scale_g), acc_g);
+    acc_g = q4_mfma(st.a[1], dequant8<true>(st.qg, scale_g), acc_g);
+    if constexpr (SWIGLU) {
+      const _Float16 su = __builtin_bit_cast(h2, st.su)[0];
+      const h2 scale_u = {su, su};
+      acc_u = q4_mfma(st.a[0], dequant8<false>(st.qu, scale_u), acc_u);
+      acc_u = q4_mfma(st.a[1], dequant8<true>(st.qu, scale_u), acc_u);
+    }
+  };
+  Stage ring[kQ4Ahead];
+  // The waits count loads in issue order: the compiler must not move them across blocks.
+#pragma unroll
+  for (int j = 0; j < kQ4Ahead; ++j) {
+    load(ring[j], j);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // Block kb sits in stage kb % kQ4Ahead; the loads of the kQ4Ahead - 1 blocks after it may still
+  // be in flight when it is used (loads retire in issue order), then its stage takes block
+  // kb + kQ4Ahead.
+  constexpr int kWait = (kQ4Ahead - 1) * kOps;
+  static_assert(kWait < 64, "vmcnt is 6 bits");
+  for (int kb = 0; kb < kblocks; kb += kQ4Ahead) {
+#pragma unroll
+    for (int j = 0; j < kQ4Ahead; ++j) {
+      __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8) | (kWait & 15) | ((kWait >> 4) << 14));
+      if (kb + j < kblocks) mma(ring[j]);
+      __builtin_amdgcn_sched_barrier(0);
+      load(ring[j], kb + j + kQ4Ahead);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+
+  // D (32 x 32): lane holds column l32 and rows 8 (r / 4) + 4 hl + r % 4 -- as the tiled kernel.
+  const int n = n0 + l32;
+  if (n >= n_out) return;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int m = m0 + 8 * (r >> 2) + 4 * hl + (r & 3);
+    const uint32_t off = m < M ? ((uint32_t)m * (uint32_t)ldy + (uint32_t)n) * 2u : 0x80000000u;
+    if constexpr (SWIGLU)
+      q4_store_b16(swiglu_value((_Float16)acc_g[r], (_Float16)acc_u[r]), yrs, off);
+    else
+      q4_store_b16((_Float16)acc_g[r], yrs, off);
+  }
+}
+
+template <bool SWIGLU>
+void launch_q4_direct(const _Float16* x, int64_t ldx, int M, int K, const uint8_t* w, uint32_t w_bytes, int N,
+                      _Float16* y, int64_t ldy, hipStream_t stream) {
+  const int n_out = SWIGLU ? N / 2 : N;
+  const int blocks_m = (M + 31) / 32, blocks = blocks_m * ((n_out + 31) / 32);
+  hipLaunchKernelGGL((q4_direct_kernel<SWIGLU>), dim3((unsigned)blocks), dim3(64), 0, stream, x, ldx, M,
+                     K, w, w_bytes, N, y, ldy, blocks_m, blocks);
+}
+
 // Grid: 8 * ceil(tiles / 8) workgroups of 256 threads (the surplus ones exit at once), 128 x 128
 // tiles, or 64 x 128 when the launch has fewer than kQ4SmallLaunch 128 x 128 tiles.
 template <bool SWIGLU, int BM>
@@ -292,7 +416,10 @@ template <bool SWIGLU>
 hipError_t launch_q4(const _Float16* x, int64_t ldx, int M, int K, const uint8_t* w, uint32_t w_bytes, int N,
                      _Float16* y, int64_t ldy, hipStream_t stream) {
   const int64_t big_tiles = (int64_t)((M + 127) / 128) * ((N + kQ4TileN - 1) / kQ4TileN);
-  if (big_tiles < kQ4SmallLaunch)
+  const int n_out = SWIGLU ? N / 2 : N;
+  if ((int64_t)((M + 31) / 32) * ((n_out + 31) / 32) <= kQ4DirectBlocks)
+    launch_q4_direct<SWIGLU>(x, ldx, M, K, w, w_bytes, N, y, ldy, stream);
+  else if (big_tiles < kQ4SmallLaunch)
     launch_q4_shape<SWIGLU, 1>(x, ldx, M, K, w, w_bytes, N, y, ldy, stream);
   else
     launch_q4_shape<SWIGLU, 2>(x, ldx, M, K, w, w_bytes, N, y, ldy, stream);

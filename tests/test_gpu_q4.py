@@ -135,22 +135,28 @@ def test_q4_matmul_swiglu_equals_the_two_launches(ctx, oracle, m, k, n_inter):
 
 
 def test_q4_rows_do_not_depend_on_the_launch_shape(ctx, oracle):
-    """Launches with fewer than 256 tiles of 128x128 use 64-row workgroup tiles, larger ones
-    128-row tiles; every output element is computed the same way in both (the same K blocks and
-    MFMA order), so the first 64 rows alone equal the same rows of a 1100-row launch bit for bit
-    -- the model's batch invariance rests on this -- for the plain and the fused gate/up
-    projections."""
+    """Three kernels serve one projection, chosen by the launch's size: up to 512 output blocks of
+    32 x 32 the one-wavefront-per-block kernel, then the tiled kernel with 64-row tiles (fewer
+    than 160 tiles of 128 x 128), then 128-row tiles.  Every output element is computed the same
+    way in all three (the same K blocks and MFMA order), so rows 0..63 of a 64-row, a 300-row and
+    an 1100-row launch are equal bit for bit -- the model's batch invariance rests on this -- for
+    the plain and the fused gate/up projections."""
     rng = np.random.default_rng(5)
     k, n = 256, 4096
     packed = random_compact(rng, n, k)
     x = rng.standard_normal((1100, k)).astype(np.float16)
-    big = run_q4(ctx, x, packed, k, n)        # 9 x 32 = 288 tiles: 128-row tiles
-    small = run_q4(ctx, x[:64], packed, k, n)  # 1 x 32 tiles: 64-row tiles
+    big = run_q4(ctx, x, packed, k, n)          # 9 x 32 = 288 tiles: 128-row tiles
+    mid = run_q4(ctx, x[:300], packed, k, n)    # 3 x 32 = 96 tiles: 64-row tiles
+    small = run_q4(ctx, x[:64], packed, k, n)   # 2 x 128 = 256 blocks: one wavefront per block
     check(oracle, big, x, packed, k, n, "q4 1100 rows")
+    check(oracle, small, x[:64], packed, k, n, "q4 64 rows")
     assert np.array_equal(big[:64].view(np.uint16), small.view(np.uint16))
+    assert np.array_equal(mid[:64].view(np.uint16), small.view(np.uint16))
     big_f = run_q4_swiglu(ctx, x, packed, k, n // 2)
-    small_f = run_q4_swiglu(ctx, x[:64], packed, k, n // 2)
+    mid_f = run_q4_swiglu(ctx, x[:300], packed, k, n // 2)
+    small_f = run_q4_swiglu(ctx, x[:64], packed, k, n // 2)  # 2 x 64 = 128 blocks
     assert np.array_equal(big_f[:64].view(np.uint16), small_f.view(np.uint16))
+    assert np.array_equal(mid_f[:64].view(np.uint16), small_f.view(np.uint16))
 
 
 def test_q4_matmul_invalid_arguments(ctx, qattn):
