@@ -218,10 +218,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   const int r0 = 4 * wave + (lane >> 4), pc = lane & 15;
   const uint32_t koff = (uint32_t)r0 * kstride_b + (uint32_t)((pc ^ r0) << 4);
   const uint32_t voff = (uint32_t)r0 * vstride_b + (uint32_t)((pc ^ ((r0 & 3) << 2)) << 4);
-  // Key tile `kt` of a sequence of S rows starting at `base` (kt * kTileK < S always).
+  // Key tile `kt` of a sequence of S rows starting at `base` (kt * kTileK < S, or S = 0 for an
+  // empty range).
   auto tile_rsrc = [&](const char* base, uint32_t stride_b, int kt, int S) {
     const int kb = kt * kTileK;
-    return make_rsrc(base + (int64_t)kb * stride_b, (uint32_t)(S - kb) * stride_b);
+    return make_rsrc(base + (int64_t)kb * stride_b, S > kb ? (uint32_t)(S - kb) * stride_b : 0u);
   };
   auto load_part = [&](char* dst, __amdgpu_buffer_rsrc_t rs, uint32_t stride_b, uint32_t off, int j) {
     // The add stays here (not hoisted into four loop-invariant registers).
@@ -267,25 +268,27 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
 
   // The loads that start a work item: this wave's Q rows into qreg, K tiles 0 and 1 into sK0 /
   // sK1 (tile 0 twice for a one-tile item, so the instruction count never varies).  Exactly
-  // kPrefetchOps vector-memory instructions per lane.
-  auto start_loads = [&](const WorkItem& w) {
+  // kPrefetchOps vector-memory instructions per lane; with real = false every buffer range is
+  // empty (the instructions read nothing and write zeros).
+  auto start_loads = [&](const WorkItem& w, bool real) {
     const int S = w.seq_len, kvh = w.seq_kvh & 15, q0 = w.q_block * kBlockQ;
     const TileRanges t = key_tiles(q0, min(S, q0 + kBlockQ) - 1, S, mask);
     const int tb = w.tile_begin, t1 = w.tile_end - w.tile_begin > 1 ? tb + 1 : tb;
     const char* qhead = reinterpret_cast<const char*>(p.q) + (uint64_t)w.seq_start * qstride_b +
                         (kvh * kGroup + head_in_group) * kRowBytes;
-    const auto rs = make_rsrc(qhead, (uint32_t)S * qstride_b);
+    const auto rs = make_rsrc(qhead, real ? (uint32_t)S * qstride_b : 0u);
     const uint32_t row_off = (uint32_t)(q0 + wave_q + lq) * qstride_b + 16u * hl;
 #pragma unroll
     for (int st = 0; st < 8; ++st)
       qreg[st] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(rs, row_off + 32u * st, 0, 0));
     const char* kb = reinterpret_cast<const char*>(p.k) + (uint64_t)w.seq_start * kstride_b + kvh * kRowBytes;
-    load_tile(sK0, kb, kstride_b, koff, t.at(tb), S);
-    load_tile(sK1, kb, kstride_b, koff, t.at(t1), S);
+    load_tile(sK0, kb, kstride_b, koff, t.at(tb), real ? S : 0);
+    load_tile(sK1, kb, kstride_b, koff, t.at(t1), real ? S : 0);
   };
 
   // ---- per-entry state (uniform over the workgroup except q_pos).  Local tile it is key tile
   // tiles.at(t0 + it) of the item; an unsplit entry has t0 = 0 and ntiles = tiles.count().
+  bool has_next = false;
   int seq_start = 0, S = 1, kvh = 0, seq = 0, wq0 = 0, wq1 = 0, q_pos = 0, ps = 0, ws = 0, ntiles = 0, t0 = 0;
   TileRanges tiles{};
   const char* kbase = nullptr;
@@ -496,10 +499,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
       if (kload) load_tile(kfree, kbase, kstride_b, koff, tiles.at(t0 + it + 2), S);
       load_tile(vfree, vbase, vstride_b, voff, tiles.at(t0 + it), S);
     }
-    // The slot's last item re-loads its own Q / K(0) / K(1) as the "next" item (valid
-    // addresses, never used), so every path issues the same vector-memory instruction count and
-    // the waits below stay exact.
-    if (last) start_loads(work(next_index));
+    // The slot's last item issues the same loads for its own Q / K(0) / K(1) as the "next"
+    // item, over empty buffer ranges: they return zeros without touching memory (the re-read
+    // of data long evicted from L2 was 13 MB of the 16x500 launch's HBM reads), and every path
+    // issues the same vector-memory instruction count, so the waits below stay exact.
+    if (last) start_loads(work(next_index), has_next);
     if (!tile_full(kb, wq0, wq1, S, mask)) apply_mask(s_cur, kb);
     if constexpr (MASKBITS) record_mask(s_cur, kb);
     if (!last) {
@@ -560,13 +564,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
 
-  start_loads(work(i_begin));
+  start_loads(work(i_begin), true);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   qk(sK0, sA, no_hook);  // S(0) of the first entry
   for (int wi = i_begin; wi < i_end; ++wi) {
     const WorkItem cur = work(wi);
-    const int next_index = wi + 1 < i_end ? wi + 1 : wi;
+    has_next = wi + 1 < i_end;
+    const int next_index = has_next ? wi + 1 : wi;
     seq_start = cur.seq_start;
     S = cur.seq_len;
     kvh = cur.seq_kvh & 15;
