@@ -480,6 +480,61 @@ def model_timing(reps, names=("full", "sparse", "cfg4", "cfg1", "cfg3")):
     ctx.close()
 
 
+def timeline_report(names):
+    """Per-workgroup phase timeline of the attention launch (qattn_debug_run_timeline: the
+    kernel's timeline variant stamps s_memrealtime, 100 MHz, at fixed points).  Each workload's
+    28 layers run 3 times back to back, then layers 0..26 once more and layer 27 under the
+    timeline, so its inputs are HBM-resident like every timed launch's.  One JSON line per
+    workload: slot start / prologue / end spread, and per entry phase durations (median, mean,
+    p90 in us) over the slots' first 15 entries."""
+    q = load_binding()
+    ctx = q.Context(0)
+    for name in names:
+        w = Workload(ctx, q, name)
+        for _ in range(3):
+            w.encode_all()
+        for r in w.runs[:-1]:
+            r.encode()
+        st = w.runs[-1].timeline().astype(np.int64)
+        d = w.runs[-1].desc
+        entries, _ = q.plan_describe(d)
+        slots = q.plan_slots(d)
+        nslots = len(slots) - 1
+        assert st.shape[0] == nslots, (st.shape, nslots)
+        used = [b for b in range(nslots) if slots[b + 1] > slots[b]]
+        t0 = min(st[b, 0] for b in used)
+        us = lambda a, b: ((a - b) % (1 << 32)) * 0.01
+        ph = {k: [] for k in ("tile_body_per_tile", "entry_top_to_first_barrier", "last_tile_next_loads_issue",
+                              "last_tile_softmax_and_last_pv", "handover_wait", "stage_rows_and_next_s0",
+                              "row_stores")}
+        starts, prologue, ends, dur = [], [], [], []
+        for b in used:
+            starts.append(us(st[b, 0], t0))
+            prologue.append(us(st[b, 1], st[b, 0]))
+            ends.append(us(st[b, 127], t0))
+            dur.append(us(st[b, 127], st[b, 0]))
+            for e in range(min(15, slots[b + 1] - slots[b])):
+                t = st[b, 2 + 8 * e: 10 + 8 * e]
+                n = int(entries[slots[b] + e][5] - entries[slots[b] + e][4])
+                if n >= 2:
+                    ph["tile_body_per_tile"].append(us(t[2], t[1]) / (n - 1))
+                ph["entry_top_to_first_barrier"].append(us(t[1], t[0]))
+                ph["last_tile_next_loads_issue"].append(us(t[3], t[2]))
+                ph["last_tile_softmax_and_last_pv"].append(us(t[4], t[3]))
+                ph["handover_wait"].append(us(t[5], t[4]))
+                ph["stage_rows_and_next_s0"].append(us(t[6], t[5]))
+                ph["row_stores"].append(us(t[7], t[6]))
+        stat = lambda a: {"median": round(float(np.median(a)), 3), "mean": round(float(np.mean(a)), 3),
+                          "p90": round(float(np.percentile(a, 90)), 3)} if len(a) else None
+        print(json.dumps({"timeline": "attn_fwd_kernel", "workload": name, "slots": len(used),
+                          "entries": int(slots[-1]), "split_items": int(w.info.split_items),
+                          "slot_start_us": stat(starts), "prologue_us": stat(prologue), "slot_end_us": stat(ends),
+                          "slot_end_max_us": round(max(ends), 3), "slot_duration_us": stat(dur),
+                          "per_entry_us": {k: stat(v) for k, v in ph.items()}}), flush=True)
+        w.free()
+    ctx.close()
+
+
 MATRIX_LENGTHS = (15, 50, 150, 500, 1500, 5000)
 
 
@@ -568,10 +623,16 @@ def main():
                     help="only time N launches of the fused QK-norm + RoPE producer and exit")
     ap.add_argument("--model", type=int, default=0, metavar="N",
                     help="only time N runs of the whole 28-layer forward (synthetic weights) per config and exit")
+    ap.add_argument("--timeline", action="store_true",
+                    help="only print the attention kernel's per-workgroup phase timeline (qattn_debug_run_timeline) "
+                         "for the headline workloads and exit")
     ap.add_argument("--model-matrix", type=int, default=0, metavar="N",
                     help="only run the reference's single / 16-request matrix at 15..5000 tokens through "
                          "the 28-layer forward, N rounds each, and exit")
     args = ap.parse_args()
+    if args.timeline:
+        timeline_report(["full", "sparse", "sparse_bi"] if args.workload == "both" else [args.workload])
+        return
     if args.model_matrix:
         model_matrix(args.model_matrix)
         return

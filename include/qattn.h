@@ -51,8 +51,9 @@ extern "C" {
  *    qattn_model_plan_*
  * 6: qattn_q4_matmul_swiglu; the model plan's FFN gate/up projection and SwiGLU are one launch
  * 7: qattn_run_update no longer waits for the device (two work-list images per run);
- *    qattn_debug_fail_allocs */
-#define QATTN_ABI_VERSION 7
+ *    qattn_debug_fail_allocs
+ * 8: qattn_debug_run_timeline */
+#define QATTN_ABI_VERSION 8
 
 #define QATTN_Q_HEADS 16
 #define QATTN_KV_HEADS 8
@@ -242,6 +243,19 @@ int qattn_plan_mask(int32_t L, int32_t mask, int32_t prefix, int32_t window, uin
  * Allocates a device buffer and synchronizes; a diagnostic, not for the hot path. */
 int qattn_debug_run_mask(qattn_run* run, uint32_t* host_bits, int64_t capacity_words,
                          int32_t* words_per_row);
+/* Phase timeline of one launch of a run -- no reference counterpart (a profiling aid for the
+ * attention kernel, as the reference's profile() times whole stages, model.ts:141-182).  Runs the
+ * kernel's timeline variant (same output rows; split plans: the merge kernel too) and returns
+ * 128 uint32 per slot (workgroup) b at host_stamps[128 b]: s_memrealtime ticks (100 MHz) at
+ * 0 start, 1 first loads landed, and per entry e < 15 of the slot at 2 + 8 e: +0 entry top,
+ * +1 after its first tile's barrier, +2 after its last tile's barrier, +3 after that tile issued
+ * the next entry's loads, +4 after the entry's last PV, +5 after the hand-over wait, +6 after
+ * the rows were staged (partials stored) and the next S(0) issued, +7 after the row stores
+ * (entries past 14 overwrite entry 14's); 127 end.  Unreached stamps are 0.  *slots receives
+ * the slot count; host_stamps NULL: only *slots.  capacity_words >= 128 * slots.
+ * Allocates a device buffer and synchronizes; a diagnostic, not for the hot path. */
+int qattn_debug_run_timeline(qattn_run* run, uint32_t* host_stamps, int64_t capacity_words,
+                             int32_t* slots);
 
 /* ---- producer: QK RMSNorm + RoPE  (replaces QKNormRopeKernel, ops.ts:104-166) ------------- */
 /* Reads the Q block (16 heads, columns 0..2047) and K block (8 heads, 2048..3071) of each qkvRaw

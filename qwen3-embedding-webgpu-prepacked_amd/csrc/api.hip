@@ -651,6 +651,35 @@ int qattn_debug_run_mask(qattn_run* run, uint32_t* host_bits, int64_t capacity_w
   return QATTN_OK;
 }
 
+int qattn_debug_run_timeline(qattn_run* run, uint32_t* host_stamps, int64_t capacity_words, int32_t* slots) {
+  if (!run) return fail(nullptr, QATTN_EINVAL, "run is NULL");
+  qattn_ctx* ctx = run->ctx;
+  const int32_t n = run->params.n_slots;
+  if (slots) *slots = n;
+  if (!host_stamps) return QATTN_OK;
+  const int64_t need = (int64_t)n * kTimelineStamps;
+  if (capacity_words < need)
+    return fail(ctx, QATTN_EINVAL, "capacity %lld words < %lld (%d slots x %d stamps)", (long long)capacity_words,
+                (long long)need, n, kTimelineStamps);
+  if (need == 0) return QATTN_OK;
+  DeviceGuard g(ctx->device);
+  uint32_t* dev = nullptr;
+  HIP_TRY(ctx, hipMalloc(&dev, (size_t)need * sizeof(uint32_t)));
+  AttnParams p = run->params;
+  p.timeline = dev;
+  // The attention kernel's timeline variant, then (split plans) the merge kernel, so the output
+  // rows are written as by qattn_run_encode.
+  hipError_t e = hipMemsetAsync(dev, 0, (size_t)need * sizeof(uint32_t), ctx->stream);
+  int rc = e == hipSuccess ? launch_run(run, p, ctx->stream, true) : QATTN_OK;
+  if (e == hipSuccess && rc == QATTN_OK)
+    e = hipMemcpyAsync(host_stamps, dev, (size_t)need * sizeof(uint32_t), hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess && rc == QATTN_OK) e = hipStreamSynchronize(ctx->stream);
+  (void)hipFree(dev);
+  if (rc != QATTN_OK) return rc;
+  if (e != hipSuccess) return fail(ctx, QATTN_EHIP, "run timeline: %s", hipGetErrorString(e));
+  return QATTN_OK;
+}
+
 void qattn_debug_fail_allocs(int32_t n) { g_fail_allocs.store(n > 0 ? n : 0); }
 
 int qattn_plan_mask(int32_t L, int32_t mask, int32_t prefix, int32_t window, uint32_t* host_bits) {

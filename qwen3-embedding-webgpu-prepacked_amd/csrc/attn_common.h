@@ -184,6 +184,15 @@ struct AttnParams {
   uint32_t* maskbits;
   int32_t mask_rows;   // packed tokens T
   int32_t mask_words;  // words per row: ceil(longest sequence / 32)
+  // Phase timeline only (qattn_debug_run_timeline): when non-NULL the kernel also writes
+  // kTimelineStamps s_memrealtime values (100 MHz) per workgroup b at timeline[b * kTimelineStamps]:
+  // 0 start, 1 first loads landed, per entry e < 15 at 2 + 8 e: +0 entry top, +1 after its first
+  // tile's barrier, +2 after its last tile's barrier, +3 after that tile issued the next
+  // entry's loads, +4 after its last PV, +5 after the hand-over wait, +6 after the rows were
+  // staged (or the partials stored) and the next S(0) issued, +7 after the row stores
+  // (entries past 14 share entry 14's stamps), kTimelineStamps - 1 end.  Unreached stamps stay 0.
+  uint32_t* timeline;
 };
+constexpr int kTimelineStamps = 128;
 
 }  // namespace qattn

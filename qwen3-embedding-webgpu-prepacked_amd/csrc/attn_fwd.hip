@@ -175,7 +175,8 @@ __device__ inline void flush_rows(const AttnParams& p, int seq_start, int S, int
 
 // SPLIT: the plan has split items (partial-result path compiled in).  LAST: the run writes
 // o_last rows.  MASKBITS: also report the kept keys (p.maskbits; the mask check only).
-template <bool SPLIT, bool LAST, bool MASKBITS = false>
+// TIMELINE: also record each workgroup's phase timestamps (p.timeline; qattn_debug_run_timeline).
+template <bool SPLIT, bool LAST, bool MASKBITS = false, bool TIMELINE = false>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   // K and V tiles, double buffered, 16 KiB each.  Four distinct objects (not offsets into one
   // array) with buffer choices fixed at compile time, so the compiler can see that the LDS-DMA
@@ -196,6 +197,21 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   const int i_begin = ((const_i32_t*)p.slot_begin)[blockIdx.x];
   const int i_end = ((const_i32_t*)p.slot_begin)[blockIdx.x + 1];
   if (i_begin >= i_end) return;
+
+  // Phase timestamps (TIMELINE only): s_memrealtime (100 MHz) read by thread 0 into LDS at
+  // kTimelineStamps fixed points, written out once the workgroup is done (LDS, so the vector-
+  // memory counts that the waits rely on are unchanged).
+  __shared__ uint32_t tl_stamps[TIMELINE ? kTimelineStamps : 1];
+  auto stamp = [&](int i) {
+    if constexpr (TIMELINE) {
+      if (threadIdx.x == 0) tl_stamps[i] = (uint32_t)__builtin_amdgcn_s_memrealtime();
+    }
+  };
+  if constexpr (TIMELINE) {
+    if (threadIdx.x < kTimelineStamps) tl_stamps[threadIdx.x] = 0;
+  }
+  stamp(0);
+  int tl_entry = 2;  // first stamp of the current entry: 2 + 8 min(entry, 14)
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps rsrc/M0 in SGPRs
@@ -490,6 +506,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     else
       wait_vmcnt<kStoreOps<LAST>>();
     __syncthreads();
+    if (it == 0) stamp(tl_entry + 1);
+    if (last) stamp(tl_entry + 2);
     // This iteration's tile loads: K(it+2) (if any) and V(it), one instruction per S(it+1) step
     // when there is one.
     const bool kload = it + 2 < ntiles;
@@ -504,6 +522,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     // of data long evicted from L2 was 13 MB of the 16x500 launch's HBM reads), and every path
     // issues the same vector-memory instruction count, so the waits below stay exact.
     if (last) start_loads(work(next_index), has_next);
+    if (last) stamp(tl_entry + 3);
     if (!tile_full(kb, wq0, wq1, S, mask)) apply_mask(s_cur, kb);
     if constexpr (MASKBITS) record_mask(s_cur, kb);
     if (!last) {
@@ -532,6 +551,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
       wait_vmcnt<kPrefetchOps>();
       __syncthreads();
       pv(vfree, p_cur);
+      stamp(tl_entry + 4);
     }
   };
 
@@ -567,9 +587,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   start_loads(work(i_begin), true);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  stamp(1);
   qk(sK0, sA, no_hook);  // S(0) of the first entry
   for (int wi = i_begin; wi < i_end; ++wi) {
     const WorkItem cur = work(wi);
+    tl_entry = 2 + 8 * min(wi - i_begin, 14);  // stamps 2 .. 121
+    stamp(tl_entry);
     has_next = wi + 1 < i_end;
     const int next_index = has_next ? wi + 1 : wi;
     seq_start = cur.seq_start;
@@ -606,6 +629,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     // allows for the stores still being in flight.
     if (wi + 1 < i_end) __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    stamp(tl_entry + 5);
     const bool rows = !SPLIT || cur.split < 0;
     lds_char_t* const stage = row_stage((lds_char_t*)sV0, (lds_char_t*)sV1);
     if (rows)
@@ -613,10 +637,17 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     else
       write_partial(cur);
     if (wi + 1 < i_end) qk(sK0, sA, no_hook);
+    stamp(tl_entry + 6);
     if (rows) flush_rows<LAST>(p, seq_start, S, seq, kvh * kGroup + head_in_group, wq0, stage);
+    stamp(tl_entry + 7);
   }
   // The last item's unused prefetch (LDS-DMA included) lands before the workgroup leaves.
   __builtin_amdgcn_s_waitcnt(0);
+  if constexpr (TIMELINE) {
+    stamp(kTimelineStamps - 1);
+    __syncthreads();
+    if (threadIdx.x < kTimelineStamps) p.timeline[(size_t)blockIdx.x * kTimelineStamps + threadIdx.x] = tl_stamps[threadIdx.x];
+  }
 }
 
 // Merge of split items (after attn_fwd_kernel, same stream).  Workgroup (split item i, wave w)
@@ -720,6 +751,11 @@ hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream) {
   // Plans without split items run the variant without the partial-result path (fewer live
   // registers in the tile loop).
   const dim3 grid(p.n_slots), block(kThreads);
+  if (p.timeline) {
+    if (p.n_splits > 0) hipLaunchKernelGGL((attn_fwd_kernel<true, false, false, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((attn_fwd_kernel<false, false, false, true>), grid, block, 0, stream, p);
+    return hipGetLastError();
+  }
   if (p.maskbits) {
     if (p.n_splits > 0) hipLaunchKernelGGL((attn_fwd_kernel<true, false, true>), grid, block, 0, stream, p);
     else hipLaunchKernelGGL((attn_fwd_kernel<false, false, true>), grid, block, 0, stream, p);

@@ -132,6 +132,7 @@ def lib():
         "qattn_plan_mask": (ctypes.c_int, [i32, i32, i32, i32, vp]),
         "qattn_debug_run_mask": (ctypes.c_int, [vp, vp, i64, ctypes.POINTER(i32)]),
         "qattn_debug_fail_allocs": (None, [i32]),
+        "qattn_debug_run_timeline": (ctypes.c_int, [vp, vp, i64, ctypes.POINTER(i32)]),
         "qattn_qk_norm_rope": (ctypes.c_int, [vp, vp, i64, i64, i32, vp, i32, vp,
                                               ctypes.c_double, ctypes.c_double, vp]),
         "qattn_qk_norm_rope_qkv": (ctypes.c_int, [vp, vp, i64, vp, i64, vp, i64, vp, i32, vp, vp,
@@ -283,6 +284,15 @@ class Run:
         out = np.zeros((HQ, T, words.value), dtype=np.uint32)
         _check(lib().qattn_debug_run_mask(self.handle, _np_ptr(out) if out.size else None, out.size,
                                           ctypes.byref(words)), self.ctx.handle)
+        return out
+
+    def timeline(self):
+        """Phase timestamps of one launch (qattn_debug_run_timeline): uint32 [slots, 128], 100 MHz."""
+        slots = ctypes.c_int32()
+        _check(lib().qattn_debug_run_timeline(self.handle, None, 0, ctypes.byref(slots)), self.ctx.handle)
+        out = np.zeros((slots.value, 128), dtype=np.uint32)
+        _check(lib().qattn_debug_run_timeline(self.handle, _np_ptr(out) if out.size else None, out.size,
+                                              ctypes.byref(slots)), self.ctx.handle)
         return out
 
     def destroy(self):

@@ -134,7 +134,7 @@ test('packVarlen / cuSeqlensOf offsets', () => {
 
 test('N-API addon loads; host-side planning and validation work without a GPU', () => {
   const addon = loadAddon();
-  assert.strictEqual(addon.abiVersion(), 7);
+  assert.strictEqual(addon.abiVersion(), 8);
   const plan = addon.planDescribe({ q: 1, k: 1, v: 1, o: 1, cuSeqlens: new Int32Array([0, 50, 550]) });
   assert.strictEqual(plan.info.tokens, 550);
   assert.strictEqual(plan.info.pairs, 1275 + 125250);
