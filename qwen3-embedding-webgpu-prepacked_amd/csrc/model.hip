@@ -28,6 +28,17 @@ constexpr int kQkvWidth = kQHeads * kHeadDim + 2 * kKVHeads * kHeadDim;  // 4096
 constexpr int kQWidth = kQHeads * kHeadDim;                              // 2048
 constexpr int kKWidth = kKVHeads * kHeadDim;                             // 1024
 constexpr int64_t kEmbdRowBytes = (int64_t)kHidden / 256 * QATTN_Q6K_BLOCK_BYTES;  // 840
+// The split workspace a plan of max_tokens needs: the largest the output (K = 2048) and down
+// (K = 3072) projections ask for at any batch size up to max_tokens.
+size_t max_split_bytes(int32_t max_tokens) {
+  size_t best = 0;
+  for (int32_t M = 1; M <= max_tokens; ++M) {
+    const size_t a = q4_split_bytes(M, kQWidth, kHidden), b = q4_split_bytes(M, kInter, kHidden);
+    if (!a && !b && M > 64) break;  // past the split range (it ends where the tiles stop being few)
+    best = std::max(best, std::max(a, b));
+  }
+  return best;
+}
 }  // namespace
 
 struct qattn_model {
@@ -51,6 +62,8 @@ struct qattn_model_plan {
   void* ffn = nullptr;         // SwiGLU output        [T][3072]
   qattn_run* run = nullptr;
   std::vector<int32_t> planned_cu;  // the batch the attention run is planned for
+  float* gemm_ws = nullptr;         // fp32 partials of the split output / down projections
+  size_t gemm_ws_bytes = 0;
 };
 
 extern "C" {
@@ -174,7 +187,7 @@ void free_plan(qattn_model_plan* p) {
   qattn_ctx* ctx = p->model->ctx;
   DeviceGuard g(ctx->device);
   (void)hipStreamSynchronize(ctx->stream);
-  void* bufs[] = {p->ids, p->x, p->normalized, p->qkv, p->q, p->k, p->attn, p->delta, p->ffn};
+  void* bufs[] = {p->ids, p->x, p->normalized, p->qkv, p->q, p->k, p->attn, p->delta, p->ffn, p->gemm_ws};
   for (void* b : bufs)
     if (b) (void)hipFree(b);
   delete p;
@@ -243,8 +256,8 @@ int enqueue(qattn_model_plan* p, const int32_t* cu, int32_t nseq, float* out, in
     STAGE_TRY(qattn_run_encode(p->run, s));
     end();
     begin(QATTN_STAGE_ATTENTION_OUTPUT);
-    STAGE_TRY(qattn_q4_matmul(ctx, p->attn, kQWidth, (int32_t)T, kQWidth, w.attn_output, w.attn_output_bytes, kHidden,
-                              p->delta, kHidden, s));
+    STAGE_TRY(q4_matmul_ws(ctx, p->attn, kQWidth, (int32_t)T, kQWidth, w.attn_output, w.attn_output_bytes, kHidden,
+                           p->delta, kHidden, s, p->gemm_ws, p->gemm_ws_bytes));
     end();
     begin(QATTN_STAGE_POST_ATTENTION_NORM);
     STAGE_TRY(qattn_rmsnorm(ctx, p->x, kHidden, p->delta, kHidden, w.ffn_norm, p->normalized, kHidden, T, kHidden,
@@ -259,8 +272,8 @@ int enqueue(qattn_model_plan* p, const int32_t* cu, int32_t nseq, float* out, in
     begin(QATTN_STAGE_SWIGLU);
     end();
     begin(QATTN_STAGE_FFN_DOWN);
-    STAGE_TRY(qattn_q4_matmul(ctx, p->ffn, kInter, (int32_t)T, kInter, w.ffn_down, w.ffn_down_bytes, kHidden, p->delta,
-                              kHidden, s));
+    STAGE_TRY(q4_matmul_ws(ctx, p->ffn, kInter, (int32_t)T, kInter, w.ffn_down, w.ffn_down_bytes, kHidden, p->delta,
+                           kHidden, s, p->gemm_ws, p->gemm_ws_bytes));
     end();
     begin(QATTN_STAGE_POST_FFN_NORM);
     STAGE_TRY(qattn_rmsnorm(ctx, p->x, kHidden, p->delta, kHidden, next_norm, p->normalized, kHidden, T, kHidden,
@@ -330,8 +343,11 @@ int qattn_model_plan_create(qattn_model* model, int32_t max_tokens, int32_t max_
                 {&p->normalized, T * kHidden * 2},             {&p->qkv, T * kQkvWidth * 2},
                 {&p->q, T * kQWidth * 2},                      {&p->k, T * kKWidth * 2},
                 {&p->attn, T * kQWidth * 2},                   {&p->delta, T * kHidden * 2},
-                {&p->ffn, T * kInter * 2}};
+                {&p->ffn, T * kInter * 2},
+                // the largest split workspace any batch of this plan asks for (0 when none splits)
+                {reinterpret_cast<void**>(&p->gemm_ws), p->gemm_ws_bytes = max_split_bytes(max_tokens)}};
     for (const Buf& b : bufs) {
+      if (!b.bytes) continue;
       const hipError_t e = hipMalloc(b.ptr, b.bytes);
       if (e != hipSuccess) {
         free_plan(p);

@@ -31,6 +31,11 @@ __device__ inline half_t swiglu_value(half_t g, half_t u) {
   return (half_t)v;
 }
 
+// Bytes of fp32 partials a Q4_0 projection of this shape splits its K chunks into (0: the
+// shape does not split; q4_matmul.hip).  A caller that passes a workspace of at least this size
+// gets the split launch; the result is bit for bit the unsplit one's.
+size_t q4_split_bytes(int M, int K, int N);
+
 // out = silu(gate) * up for rows of [gate (width) | up (width)], width a multiple of 8.
 hipError_t launch_swiglu(const half_t* gate_up, int64_t gu_stride, half_t* out, int64_t out_stride, int64_t rows,
                          int width, hipStream_t stream);

@@ -51,6 +51,16 @@ constexpr int kQ4Record = 20;   // bytes per (row, 32-column block)
 // at M = 500-1,419, slower above about 160 tiles).  Each output element is computed the same way
 // in both.
 constexpr int kQ4SmallLaunch = 160;
+// Fixed K split: every output element is the fp32 sum, in chunk order, of MFMA chains over
+// chunks of kQ4ChunkBlocks 32-column K blocks, each chain from a zero accumulator:
+// y = f16((c0 + c1) + c2) for K = 3072.  The split depends on K alone, so a row's result does
+// not depend on the batch whichever way a launch computes it: in registers (every chunk in one
+// workgroup, a second accumulator set) or, for launches with few tiles, one workgroup per
+// (tile, chunk) writing fp32 partials that q4_reduce_kernel sums in the same order.
+constexpr int kQ4ChunkBlocks = 32;
+// Launches with fewer than this many 64 x 128 tiles and more than one chunk split the chunks
+// over workgroups when the caller provides a workspace (chunks x M x N fp32).
+constexpr int kQ4SplitTiles = 256;
 
 __device__ inline __amdgpu_buffer_rsrc_t q4_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
@@ -102,11 +112,15 @@ __device__ inline f16x q4_mfma(h8 a, h8 b, f16x c) { return __builtin_amdgcn_mfm
 // columns: the workgroup of tile column tn takes gate rows 64 tn .. +63 and the matching up rows
 // (B rows 0-31 gate, 32-63 up, 64-95 gate, 96-127 up), so every wave holds the gate and up
 // accumulators of the same 32 features in the same lanes and applies swiglu_value to them.
-template <bool SWIGLU, int BM>
+// CH = 0: K within one chunk (one chain); 1: every chunk in this workgroup (a second set of
+// accumulators holds the finished chunks' sum); 2: one chunk per workgroup (work unit t =
+// tile * chunks + chunk), its chain stored as fp32 to part[chunk][m][n].
+template <bool SWIGLU, int BM, int CH>
 __global__ __launch_bounds__(256, 2) void q4_matmul_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, int K,
                                                            const uint8_t* __restrict__ w, uint32_t w_bytes, int N,
                                                            _Float16* __restrict__ y, int64_t ldy, int tiles_n,
-                                                           int tiles_total, int per_xcd) {
+                                                           int tiles_total, int per_xcd, float* __restrict__ part,
+                                                           int chunks) {
   // Double-buffered A and B tiles: four distinct objects, each buffer choice fixed at compile
   // time, so the compiler sees that LDS-DMA writes in flight never alias the tile being read.
   constexpr int kTileM = 64 * BM;
@@ -117,8 +131,9 @@ __global__ __launch_bounds__(256, 2) void q4_matmul_kernel(const _Float16* __res
 
   // Tile of this workgroup: XCD b % 8 owns tiles [xcd * per_xcd, (xcd + 1) * per_xcd).
   const int b = blockIdx.x;
-  const int t = (b & 7) * per_xcd + (b >> 3);
-  if (t >= tiles_total) return;
+  const int u = (b & 7) * per_xcd + (b >> 3);
+  if (u >= tiles_total) return;
+  const int t = CH == 2 ? u / chunks : u;
   const int m0 = (t / tiles_n) * kTileM, n0 = (t % tiles_n) * kQ4TileN;
 
   const int tid = threadIdx.x;
@@ -127,6 +142,9 @@ __global__ __launch_bounds__(256, 2) void q4_matmul_kernel(const _Float16* __res
   const int l32 = lane & 31, hl = lane >> 5;
   const int wr = 32 * BM * (wave & 1), wc = 64 * (wave >> 1);  // this wave's 32 BM x 64 inside the tile
   const int kblocks = K >> 5;
+  // K blocks of this workgroup: all of them, or (CH == 2) one chunk.
+  const int kb_first = CH == 2 ? (u % chunks) * kQ4ChunkBlocks : 0;
+  const int kb_end = CH == 2 ? min(kb_first + kQ4ChunkBlocks, kblocks) : kblocks;
 
   const auto xrs = q4_rsrc(x, (uint32_t)M * (uint32_t)ldx * 2u);  // rows >= M read as zeros
   const auto wrs = q4_rsrc(w, w_bytes);
@@ -144,7 +162,7 @@ __global__ __launch_bounds__(256, 2) void q4_matmul_kernel(const _Float16* __res
     a_src[j] = (uint32_t)(m0 + row) * (uint32_t)ldx * 2u + 16u * chunk;
   }
   auto load_a = [&](char* dst, int kb) {
-    kb = kb < kblocks ? kb : kblocks - 1;  // past the end: re-read the last block (never used)
+    kb = kb < kb_end ? kb : kb_end - 1;  // past the end: re-read the last block (never used)
 #pragma unroll
     for (int j = 0; j < BM; ++j) q4_dma16(xrs, dst + 1024 * (BM * wave + j), a_src[j] + (uint32_t)kb * 64u);
   };
@@ -162,7 +180,7 @@ __global__ __launch_bounds__(256, 2) void q4_matmul_kernel(const _Float16* __res
     u2 q;
   };
   auto load_w = [&](WRegs& r, int kb) {
-    kb = kb < kblocks ? kb : kblocks - 1;
+    kb = kb < kb_end ? kb : kb_end - 1;
     const uint32_t off = w_rec + (uint32_t)kb * w_step;
     r.scale = __builtin_amdgcn_raw_buffer_load_b32(wrs, off, 0, 0);
     r.q = __builtin_amdgcn_raw_buffer_load_b64(wrs, off + 4u + 8u * bhalf, 0, 0);
@@ -197,13 +215,16 @@ __global__ __launch_bounds__(256, 2) void q4_matmul_kernel(const _Float16* __res
   };
   // The MFMA order of an output block -- s, then its K blocks in turn -- is the same for BM = 1
   // and 2, so rows do not depend on the tile height a launch picks.
-  auto mma = [&](const Frags& f) {
+  // fresh: the first K block of a chain (CH == 1 chunks after the first): step 0 accumulates onto
+  // the inline constant 0, which is what the zeroed accumulators would add.
+  auto mma = [&](const Frags& f, auto fresh) {
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
       for (int mb = 0; mb < BM; ++mb)
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = q4_mfma(f.a[mb][s], f.b[nb][s], acc[mb][nb]);
+        for (int nb = 0; nb < 2; ++nb)
+          acc[mb][nb] = q4_mfma(f.a[mb][s], f.b[nb][s], decltype(fresh)::value && s == 0 ? f16x{} : acc[mb][nb]);
   };
 
   // ---- pipeline.  Step kb (P = kb & 1, compile time): issue A(kb+1) into sA<1-P> and W(kb+3)
@@ -214,15 +235,15 @@ __global__ __launch_bounds__(256, 2) void q4_matmul_kernel(const _Float16* __res
   // were consumed by MFMAs before the previous barrier.  Every load is issued (clamped past the
   // end), so the counts are the same on every path.
   WRegs wreg[4];
-  load_a(sA0, 0);
-  load_w(wreg[0], 0);
-  load_w(wreg[1], 1);
-  load_w(wreg[2], 2);
+  load_a(sA0, kb_first);
+  load_w(wreg[0], kb_first);
+  load_w(wreg[1], kb_first + 1);
+  load_w(wreg[2], kb_first + 2);
   __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8) | 4);  // vmcnt(4): A(0), W(0) landed
   store_b(sB0, wreg[0]);
   __syncthreads();
   read_frags(sA0, sB0, frag[0]);
-  auto step = [&](auto pconst, auto wcur, auto wnext, int kb) {
+  auto step = [&](auto pconst, auto wcur, auto wnext, int kb, auto fresh) {
     constexpr int P = decltype(pconst)::value;
     constexpr int WN = decltype(wnext)::value;   // stage of W(kb+1)
     constexpr int WA = decltype(wcur)::value;    // stage receiving W(kb+3)
@@ -231,7 +252,7 @@ __global__ __launch_bounds__(256, 2) void q4_matmul_kernel(const _Float16* __res
     load_a(a_nxt, kb + 1);
     load_w(wreg[WA], kb + 3);
     store_b(b_nxt, wreg[WN]);
-    if (kb < kblocks) mma(frag[P]);
+    if (kb < kb_end) mma(frag[P], fresh);
     __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8) | 2);  // vmcnt(2)
     __syncthreads();
     read_frags(a_nxt, b_nxt, frag[1 - P]);
@@ -240,17 +261,66 @@ __global__ __launch_bounds__(256, 2) void q4_matmul_kernel(const _Float16* __res
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
   using I3 = std::integral_constant<int, 3>;
-  for (int kb = 0; kb < kblocks; kb += 4) {
-    step(I0{}, I3{}, I1{}, kb);
-    step(I1{}, I0{}, I2{}, kb + 1);
-    step(I0{}, I1{}, I3{}, kb + 2);
-    step(I1{}, I2{}, I0{}, kb + 3);
+  // Chunks of kQ4ChunkBlocks (a multiple of the 4-step group, so the steps' compile-time
+  // buffer and register-stage choices follow from kb as before); CH == 1 folds each finished
+  // chunk into tot and starts the next chain from zero.
+  using Fresh = std::integral_constant<bool, true>;
+  using Cont = std::integral_constant<bool, false>;
+  auto four_steps = [&](int kb, auto fresh) {
+    step(I0{}, I3{}, I1{}, kb, fresh);
+    step(I1{}, I0{}, I2{}, kb + 1, Cont{});
+    step(I0{}, I1{}, I3{}, kb + 2, Cont{});
+    step(I1{}, I2{}, I0{}, kb + 3, Cont{});
+  };
+  f16x tot[CH == 1 ? BM : 1][2];
+  if constexpr (CH == 1) {
+    // Chunk 0 into acc, copied to tot; every later chunk a fresh chain in acc, added to tot.
+    for (int kb = 0; kb < kQ4ChunkBlocks; kb += 4) four_steps(kb, Cont{});
+#pragma unroll
+    for (int mb = 0; mb < BM; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) tot[mb][nb] = acc[mb][nb];
+    for (int c0 = kQ4ChunkBlocks; c0 < kblocks; c0 += kQ4ChunkBlocks) {
+      const int c1 = min(c0 + kQ4ChunkBlocks, kblocks);
+      four_steps(c0, Fresh{});
+      for (int kb = c0 + 4; kb < c1; kb += 4) four_steps(kb, Cont{});
+#pragma unroll
+      for (int mb = 0; mb < BM; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) tot[mb][nb] = tot[mb][nb] + acc[mb][nb];
+    }
+  } else {
+    for (int kb = kb_first; kb < kb_end; kb += 4) four_steps(kb, Cont{});
   }
   __builtin_amdgcn_s_waitcnt(0);  // the clamped loads past the end land before the LDS is released
+  if constexpr (CH == 1) {
+#pragma unroll
+    for (int mb = 0; mb < BM; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = tot[mb][nb];
+  }
 
   // D (32 x 32 per block): lane holds column l32 and rows 8 (r / 4) + 4 hl + r % 4, r = 0..15.
   // Columns >= N are skipped here; rows >= M fall outside the Y resource and are dropped.
   const int wm = m0 + wr, wn = n0 + wc;
+  if constexpr (CH == 2) {
+    // This chunk's chains, fp32, to part[chunk][m][n] (rows >= M and columns >= N skipped).
+    float* const pc = part + (size_t)(u % chunks) * (size_t)M * (size_t)N;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const int n = wn + 32 * nb + l32;
+      if (n < N) {
+#pragma unroll
+        for (int mb = 0; mb < BM; ++mb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int m = wm + 32 * mb + 8 * (r >> 2) + 4 * hl + (r & 3);
+            if (m < M) pc[(size_t)m * N + n] = acc[mb][nb][r];
+          }
+      }
+    }
+    return;
+  }
   if constexpr (SWIGLU) {
     // Block nb = 0 holds gate, nb = 1 up, of output features (n0 + wc) / 2 + l32.
     const uint32_t n = (uint32_t)((wn >> 1) + l32);
@@ -300,7 +370,8 @@ __global__ __launch_bounds__(256, 2) void q4_matmul_kernel(const _Float16* __res
 constexpr int kQ4DirectBlocks = 512;
 constexpr int kQ4Ahead = 8;  // K blocks in flight per wavefront (a ring of register stages)
 
-template <bool SWIGLU>
+// CHUNKED: K spans several chunks, summed in chunk order as the tiled kernel does.
+template <bool SWIGLU, bool CHUNKED>
 __global__ __launch_bounds__(64) void q4_direct_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, int K,
                                                         const uint8_t* __restrict__ w, uint32_t w_bytes, int N,
                                                         _Float16* __restrict__ y, int64_t ldy, int blocks_m,
@@ -366,6 +437,8 @@ __global__ __launch_bounds__(64) void q4_direct_kernel(const _Float16* __restric
   // kb + kQ4Ahead.
   constexpr int kWait = (kQ4Ahead - 1) * kOps;
   static_assert(kWait < 64, "vmcnt is 6 bits");
+  static_assert(kQ4ChunkBlocks % kQ4Ahead == 0, "chunk ends fall between ring passes");
+  f16x tot_g = {}, tot_u = {};
   for (int kb = 0; kb < kblocks; kb += kQ4Ahead) {
 #pragma unroll
     for (int j = 0; j < kQ4Ahead; ++j) {
@@ -375,8 +448,23 @@ __global__ __launch_bounds__(64) void q4_direct_kernel(const _Float16* __restric
       load(ring[j], kb + j + kQ4Ahead);
       __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (CHUNKED) {
+      // End of a chunk (or of K): fold the chain into the sum and start the next from zero.
+      if ((kb + kQ4Ahead) % kQ4ChunkBlocks == 0 || kb + kQ4Ahead >= kblocks) {
+        tot_g = kb < kQ4ChunkBlocks ? acc_g : tot_g + acc_g;
+        acc_g = f16x{};
+        if constexpr (SWIGLU) {
+          tot_u = kb < kQ4ChunkBlocks ? acc_u : tot_u + acc_u;
+          acc_u = f16x{};
+        }
+      }
+    }
   }
   __builtin_amdgcn_s_waitcnt(0);
+  if constexpr (CHUNKED) {
+    acc_g = tot_g;
+    acc_u = tot_u;
+  }
 
   // D (32 x 32): lane holds column l32 and rows 8 (r / 4) + 4 hl + r % 4 -- as the tiled kernel.
   const int n = n0 + l32;
@@ -397,39 +485,78 @@ void launch_q4_direct(const _Float16* x, int64_t ldx, int M, int K, const uint8_
                       _Float16* y, int64_t ldy, hipStream_t stream) {
   const int n_out = SWIGLU ? N / 2 : N;
   const int blocks_m = (M + 31) / 32, blocks = blocks_m * ((n_out + 31) / 32);
-  hipLaunchKernelGGL((q4_direct_kernel<SWIGLU>), dim3((unsigned)blocks), dim3(64), 0, stream, x, ldx, M,
-                     K, w, w_bytes, N, y, ldy, blocks_m, blocks);
+  if (K / 32 > kQ4ChunkBlocks)
+    hipLaunchKernelGGL((q4_direct_kernel<SWIGLU, true>), dim3((unsigned)blocks), dim3(64), 0, stream, x, ldx, M,
+                       K, w, w_bytes, N, y, ldy, blocks_m, blocks);
+  else
+    hipLaunchKernelGGL((q4_direct_kernel<SWIGLU, false>), dim3((unsigned)blocks), dim3(64), 0, stream, x, ldx, M,
+                       K, w, w_bytes, N, y, ldy, blocks_m, blocks);
+}
+
+// y = f16(part[0] + part[1] + ...), summed in chunk order (part: chunks x M x N fp32).
+__global__ __launch_bounds__(256) void q4_reduce_kernel(const float* __restrict__ part, int chunks, int M, int N,
+                                                        _Float16* __restrict__ y, int64_t ldy) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)M * N) return;
+  const int64_t m = i / N, n = i % N;
+  const size_t plane = (size_t)M * (size_t)N;
+  float s = part[i];
+  for (int c = 1; c < chunks; ++c) s = s + part[(size_t)c * plane + i];
+  y[m * ldy + n] = (_Float16)s;
 }
 
 // Grid: 8 * ceil(tiles / 8) workgroups of 256 threads (the surplus ones exit at once), 128 x 128
 // tiles, or 64 x 128 when the launch has fewer than kQ4SmallLaunch 128 x 128 tiles.
-template <bool SWIGLU, int BM>
+template <bool SWIGLU, int BM, int CH>
 void launch_q4_shape(const _Float16* x, int64_t ldx, int M, int K, const uint8_t* w, uint32_t w_bytes, int N,
-                     _Float16* y, int64_t ldy, hipStream_t stream) {
+                     _Float16* y, int64_t ldy, hipStream_t stream, float* part = nullptr, int chunks = 1) {
   const int tiles_m = (M + 64 * BM - 1) / (64 * BM), tiles_n = (N + kQ4TileN - 1) / kQ4TileN;
-  const int tiles = tiles_m * tiles_n, per_xcd = (tiles + 7) / 8;
-  hipLaunchKernelGGL((q4_matmul_kernel<SWIGLU, BM>), dim3((unsigned)(8 * per_xcd)), dim3(256), 0, stream, x, ldx, M,
-                     K, w, w_bytes, N, y, ldy, tiles_n, tiles, per_xcd);
+  const int units = tiles_m * tiles_n * (CH == 2 ? chunks : 1), per_xcd = (units + 7) / 8;
+  hipLaunchKernelGGL((q4_matmul_kernel<SWIGLU, BM, CH>), dim3((unsigned)(8 * per_xcd)), dim3(256), 0, stream, x, ldx,
+                     M, K, w, w_bytes, N, y, ldy, tiles_n, units, per_xcd, part, chunks);
+}
+template <bool SWIGLU, int BM>
+void launch_q4_tiled(const _Float16* x, int64_t ldx, int M, int K, const uint8_t* w, uint32_t w_bytes, int N,
+                     _Float16* y, int64_t ldy, hipStream_t stream) {
+  if (K / 32 > kQ4ChunkBlocks)
+    launch_q4_shape<SWIGLU, BM, 1>(x, ldx, M, K, w, w_bytes, N, y, ldy, stream);
+  else
+    launch_q4_shape<SWIGLU, BM, 0>(x, ldx, M, K, w, w_bytes, N, y, ldy, stream);
+}
+
+size_t q4_split_bytes(int M, int K, int N) {
+  const int chunks = (K / 32 + kQ4ChunkBlocks - 1) / kQ4ChunkBlocks;
+  const int64_t tiles = (int64_t)((M + 63) / 64) * ((N + kQ4TileN - 1) / kQ4TileN);
+  if (chunks < 2 || tiles >= kQ4SplitTiles) return 0;
+  return (size_t)chunks * (size_t)M * (size_t)N * sizeof(float);
 }
 
 template <bool SWIGLU>
 hipError_t launch_q4(const _Float16* x, int64_t ldx, int M, int K, const uint8_t* w, uint32_t w_bytes, int N,
-                     _Float16* y, int64_t ldy, hipStream_t stream) {
+                     _Float16* y, int64_t ldy, hipStream_t stream, float* ws, size_t ws_bytes) {
   const int64_t big_tiles = (int64_t)((M + 127) / 128) * ((N + kQ4TileN - 1) / kQ4TileN);
   const int n_out = SWIGLU ? N / 2 : N;
-  if ((int64_t)((M + 31) / 32) * ((n_out + 31) / 32) <= kQ4DirectBlocks)
+  const size_t split = SWIGLU ? 0 : q4_split_bytes(M, K, N);
+  if ((int64_t)((M + 31) / 32) * ((n_out + 31) / 32) <= kQ4DirectBlocks) {
     launch_q4_direct<SWIGLU>(x, ldx, M, K, w, w_bytes, N, y, ldy, stream);
-  else if (big_tiles < kQ4SmallLaunch)
-    launch_q4_shape<SWIGLU, 1>(x, ldx, M, K, w, w_bytes, N, y, ldy, stream);
-  else
-    launch_q4_shape<SWIGLU, 2>(x, ldx, M, K, w, w_bytes, N, y, ldy, stream);
+  } else if (split && ws && split <= ws_bytes) {
+    const int chunks = (K / 32 + kQ4ChunkBlocks - 1) / kQ4ChunkBlocks;
+    launch_q4_shape<SWIGLU, 1, 2>(x, ldx, M, K, w, w_bytes, N, y, ldy, stream, ws, chunks);
+    const int64_t n = (int64_t)M * N;
+    hipLaunchKernelGGL(q4_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, ws, chunks, M, N, y,
+                       ldy);
+  } else if (big_tiles < kQ4SmallLaunch) {
+    launch_q4_tiled<SWIGLU, 1>(x, ldx, M, K, w, w_bytes, N, y, ldy, stream);
+  } else {
+    launch_q4_tiled<SWIGLU, 2>(x, ldx, M, K, w, w_bytes, N, y, ldy, stream);
+  }
   return hipGetLastError();
 }
 
 hipError_t launch_q4_matmul(const _Float16* x, int64_t ldx, int M, int K, const uint8_t* w, uint32_t w_bytes, int N,
-                            _Float16* y, int64_t ldy, hipStream_t stream) {
+                            _Float16* y, int64_t ldy, hipStream_t stream, float* ws, size_t ws_bytes) {
   if (M <= 0 || N <= 0) return hipSuccess;
-  return launch_q4<false>(x, ldx, M, K, w, w_bytes, N, y, ldy, stream);
+  return launch_q4<false>(x, ldx, M, K, w, w_bytes, N, y, ldy, stream, ws, ws_bytes);
 }
 
 // y [M, n_inter] = swiglu of the [gate | up] projection; the weight has 2 n_inter rows and
@@ -437,7 +564,7 @@ hipError_t launch_q4_matmul(const _Float16* x, int64_t ldx, int M, int K, const 
 hipError_t launch_q4_matmul_swiglu(const _Float16* x, int64_t ldx, int M, int K, const uint8_t* w, uint32_t w_bytes,
                                    int n_inter, _Float16* y, int64_t ldy, hipStream_t stream) {
   if (M <= 0 || n_inter <= 0) return hipSuccess;
-  return launch_q4<true>(x, ldx, M, K, w, w_bytes, 2 * n_inter, y, ldy, stream);
+  return launch_q4<true>(x, ldx, M, K, w, w_bytes, 2 * n_inter, y, ldy, stream, nullptr, 0);
 }
 
 }  // namespace qattn

@@ -24,7 +24,7 @@ def ulps(a, b):
 class DeviceModel:
     """Synthetic weights uploaded once; the qattn_model over them."""
 
-    def __init__(self, ctx, weights):
+    def __init__(self, ctx, weights, flags=0):
         self.ctx = ctx
         self.bufs = []
         up = lambda a: self._keep(ctx.upload(np.ascontiguousarray(a)))
@@ -39,7 +39,8 @@ class DeviceModel:
                 packed = lw[name][0]
                 d[name] = (up(packed).ptr, packed.nbytes)
             self.layers.append(d)
-        self.model = ctx.model((self.embd.ptr, weights["token_embd"].nbytes), self.out_norm.ptr, self.layers)
+        self.model = ctx.model((self.embd.ptr, weights["token_embd"].nbytes), self.out_norm.ptr, self.layers,
+                               flags=flags)
 
     def _keep(self, b):
         self.bufs.append(b)
@@ -165,6 +166,32 @@ def test_model_forward_28_layers_matches_oracle(ctx):
         want = mr.forward(weights, ids, cu)
         e, c = _check_embeddings(got, want)
         print(f"28 layers, lengths {lengths}: max|err| {e:.3e}, min cos {c:.7f}", flush=True)
+    finally:
+        m.free()
+
+
+def test_model_rows_do_not_depend_on_the_batch(ctx, weights):
+    """With the batch-invariant attention plan, a request's embedding is the same bits alone and
+    in batches whose projections take other kernels: alone (120 tokens) the output and down
+    projections run the one-wavefront-per-block kernel; in 700- and 1,300-token batches they
+    split their K chunks over workgroups (fp32 partials in the plan's workspace, summed in chunk
+    order); in a 2,600-token batch they sum the chunks in registers."""
+    m = DeviceModel(ctx, weights, flags=1)
+    rng = np.random.default_rng(12)
+    probe = rng.integers(0, weights["vocab"], 120).astype(np.int32)
+    try:
+        ref = None
+        for total in (120, 700, 1300, 2600):
+            rest = total - 120
+            lengths = [120] + ([rest // 2, rest - rest // 2] if rest else [])
+            cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+            ids = np.concatenate([probe, rng.integers(0, weights["vocab"], rest).astype(np.int32)])
+            print(f"batch of {total} tokens: {lengths}", flush=True)
+            got = _run(ctx, m, ids, cu, max_tokens=2600, max_seqs=4)[0]
+            if ref is None:
+                ref = got.copy()
+                _check_embeddings(got[None], mr.forward(weights, probe, np.array([0, 120], np.int32)))
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), total
     finally:
         m.free()
 

@@ -159,6 +159,23 @@ def test_q4_rows_do_not_depend_on_the_launch_shape(ctx, oracle):
     assert np.array_equal(mid_f[:64].view(np.uint16), small_f.view(np.uint16))
 
 
+def test_q4_chunked_k_rows_do_not_depend_on_the_launch_shape(ctx, oracle):
+    """K = 3072 spans three chunks of 1024 columns, summed in chunk order.  The direct kernel
+    (64 rows: 64 output blocks), the 64-row tiled kernel (300 and 1100 rows) and the 128-row
+    tiled kernel (2600 rows: 168 tiles of 128 x 128) all hold the finished chunks in a second
+    accumulator set, so rows 0..63 agree bit for bit."""
+    rng = np.random.default_rng(6)
+    k, n = 3072, 1024
+    packed = random_compact(rng, n, k)
+    x = rng.standard_normal((2600, k)).astype(np.float16)
+    small = run_q4(ctx, x[:64], packed, k, n)
+    check(oracle, small, x[:64], packed, k, n, "q4 chunked 64 rows")
+    for m in (300, 1100, 2600):
+        got = run_q4(ctx, x[:m], packed, k, n)
+        assert np.array_equal(got[:64].view(np.uint16), small.view(np.uint16)), m
+    check(oracle, got[:200], x[:200], packed, k, n, "q4 chunked 2600 rows (first 200)")
+
+
 def test_q4_matmul_invalid_arguments(ctx, qattn):
     buf = ctx.alloc(1 << 16)
     good = dict(m=4, k=64, n=8, w_bytes=qattn.lib().qattn_q4_compact_bytes(64, 8), ldx=64, ldy=8, x_off=0)
