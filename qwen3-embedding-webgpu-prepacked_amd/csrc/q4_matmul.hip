@@ -58,9 +58,11 @@ constexpr int kQ4SmallLaunch = 160;
 // workgroup, a second accumulator set) or, for launches with few tiles, one workgroup per
 // (tile, chunk) writing fp32 partials that q4_reduce_kernel sums in the same order.
 constexpr int kQ4ChunkBlocks = 32;
-// Launches with fewer than this many 64 x 128 tiles and more than one chunk split the chunks
-// over workgroups when the caller provides a workspace (chunks x M x N fp32).
-constexpr int kQ4SplitTiles = 256;
+// Launches with fewer than this many 64 x 128 tiles (two per CU) and more than one chunk split
+// the chunks over workgroups when the caller provides a workspace (chunks x M x N fp32).  The
+// model's output and down projections split up to M = 4,095: 16 x 150 tokens forward 2.5% faster
+// than with the limit at 256 tiles, the other batch sizes unchanged.
+constexpr int kQ4SplitTiles = 512;
 
 __device__ inline __amdgpu_buffer_rsrc_t q4_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
