@@ -173,21 +173,21 @@ def test_model_forward_28_layers_matches_oracle(ctx):
 def test_model_rows_do_not_depend_on_the_batch(ctx, weights):
     """With the batch-invariant attention plan, a request's embedding is the same bits alone and
     in batches whose projections take other kernels: alone (120 tokens) the output and down
-    projections run the one-wavefront-per-block kernel; in 700- and 1,300-token batches they
+    projections run the one-wavefront-per-block kernel; in 700- and 2,600-token batches they
     split their K chunks over workgroups (fp32 partials in the plan's workspace, summed in chunk
-    order); in a 2,600-token batch they sum the chunks in registers."""
+    order); in a 4,200-token batch (beyond the split range) they sum the chunks in registers."""
     m = DeviceModel(ctx, weights, flags=1)
     rng = np.random.default_rng(12)
     probe = rng.integers(0, weights["vocab"], 120).astype(np.int32)
     try:
         ref = None
-        for total in (120, 700, 1300, 2600):
+        for total in (120, 700, 2600, 4200):
             rest = total - 120
             lengths = [120] + ([rest // 2, rest - rest // 2] if rest else [])
             cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
             ids = np.concatenate([probe, rng.integers(0, weights["vocab"], rest).astype(np.int32)])
             print(f"batch of {total} tokens: {lengths}", flush=True)
-            got = _run(ctx, m, ids, cu, max_tokens=2600, max_seqs=4)[0]
+            got = _run(ctx, m, ids, cu, max_tokens=4200, max_seqs=4)[0]
             if ref is None:
                 ref = got.copy()
                 _check_embeddings(got[None], mr.forward(weights, probe, np.array([0, 120], np.int32)))
