@@ -160,10 +160,12 @@ def test_q4_rows_do_not_depend_on_the_launch_shape(ctx, oracle):
 
 
 def test_q4_chunked_k_rows_do_not_depend_on_the_launch_shape(ctx, oracle):
-    """K = 3072 spans three chunks of 1024 columns, summed in chunk order.  The direct kernel
-    (64 rows: 64 output blocks), the 64-row tiled kernel (300 and 1100 rows) and the 128-row
-    tiled kernel (2600 rows: 168 tiles of 128 x 128) all hold the finished chunks in a second
-    accumulator set, so rows 0..63 agree bit for bit."""
+    """K = 3072 spans three chunks of 1024 columns, summed in chunk order by every kernel: the
+    direct kernel with one wavefront per chunk meeting in LDS (64 rows: 64 output blocks x 3
+    chunks), the direct kernel with one wavefront folding the chunks in turn (300 rows: 320
+    blocks, too many chunk wavefronts), the 64-row tiled kernel (1100 rows) and the 128-row tiled
+    kernel (2600 rows: 168 tiles of 128 x 128), both with a second accumulator set.  Rows 0..63
+    agree bit for bit."""
     rng = np.random.default_rng(6)
     k, n = 3072, 1024
     packed = random_compact(rng, n, k)
