@@ -377,17 +377,23 @@ constexpr int kQ4Ahead = 8;  // K blocks in flight per wavefront (a ring of regi
 // wavefront c runs chunk c's chain, the chains meet in LDS and wavefront 0 sums them in chunk
 // order, as the tiled kernel does.  CH = 2: one wavefront runs the chunks in turn and folds each
 // finished chain into a second accumulator (launches whose chunk wavefronts would crowd the CUs).
+// CH = 3 (SWIGLU, K one chunk): two wavefronts, the gate chain and the up chain, which meet in LDS
+// for the epilogue.
 constexpr int kQ4MaxChunks = 8;  // K <= 8192 on this path
 // CH = 1 up to one output block per CU.  Measured at M = 15-240 for the output and down
 // projections: 25-46% faster than one wavefront folding the chunks; with more blocks the chunk
 // wavefronts share CUs and were up to 13% slower.
 constexpr int kQ4ChunkParallelBlocks = 256;
 template <bool SWIGLU, int CH>
-__global__ __launch_bounds__(CH == 1 ? 64 * kQ4MaxChunks : 64) void q4_direct_kernel(
+__global__ __launch_bounds__(CH == 1 ? 64 * kQ4MaxChunks : CH == 3 ? 128 : 64) void q4_direct_kernel(
     const _Float16* __restrict__ x, int64_t ldx, int M, int K, const uint8_t* __restrict__ w, uint32_t w_bytes, int N,
     _Float16* __restrict__ y, int64_t ldy, int blocks_m, int blocks_total) {
+  static_assert(CH != 3 || SWIGLU, "gate/up wavefront pairs are a SWIGLU form");
   const int lane = threadIdx.x & 63, l32 = lane & 31, hl = lane >> 5;
   constexpr bool CHUNKED = CH == 1;
+  constexpr bool PAIR = CH == 3;          // this wavefront runs one of the two SWIGLU chains
+  constexpr bool BOTH = SWIGLU && !PAIR;  // this wavefront runs the gate and the up chain
+  const int half = PAIR ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : 0;  // 0 gate, 1 up
   const int chunk = CHUNKED ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : 0;
   // block g: the M blocks of one N block are consecutive (they share weight records in L2)
   const int g = blockIdx.x;
@@ -406,7 +412,9 @@ __global__ __launch_bounds__(CH == 1 ? 64 * kQ4MaxChunks : 64) void q4_direct_ke
   auto w_rec = [&](int n) {
     return ((uint32_t)(n >> 5) * (uint32_t)kblocks_all * 32u + (uint32_t)(n & 31)) * kQ4Record;
   };
-  const uint32_t wg_rec = w_rec(n0 + l32), wu_rec = SWIGLU ? w_rec(n_out + n0 + l32) : 0u;
+  const uint32_t wu_rec = SWIGLU ? w_rec(n_out + n0 + l32) : 0u;
+  // The first chain's records: the gate rows (the up rows for the second wavefront of a pair).
+  const uint32_t wg_rec = PAIR && half ? wu_rec : w_rec(n0 + l32);
   const uint32_t w_step = 32u * kQ4Record;
 
   struct Stage {
@@ -414,7 +422,7 @@ __global__ __launch_bounds__(CH == 1 ? 64 * kQ4MaxChunks : 64) void q4_direct_ke
     uint32_t sg, su;
     u2 qg, qu;
   };
-  constexpr int kOps = SWIGLU ? 6 : 4;  // vector-memory instructions per K block
+  constexpr int kOps = BOTH ? 6 : 4;  // vector-memory instructions per K block
   auto load = [&](Stage& st, int kb) {
     kb = kb < kblocks ? kb : kblocks - 1;  // past the end: re-read the last block (never used)
     const uint32_t xo = x_row + (uint32_t)kb * 64u;
@@ -423,7 +431,7 @@ __global__ __launch_bounds__(CH == 1 ? 64 * kQ4MaxChunks : 64) void q4_direct_ke
     const uint32_t go = wg_rec + (uint32_t)kb * w_step;
     st.sg = __builtin_amdgcn_raw_buffer_load_b32(wrs, go, 0, 0);
     st.qg = __builtin_amdgcn_raw_buffer_load_b64(wrs, go + 4u + 8u * hl, 0, 0);
-    if constexpr (SWIGLU) {
+    if constexpr (BOTH) {
       const uint32_t uo = wu_rec + (uint32_t)kb * w_step;
       st.su = __builtin_amdgcn_raw_buffer_load_b32(wrs, uo, 0, 0);
       st.qu = __builtin_amdgcn_raw_buffer_load_b64(wrs, uo + 4u + 8u * hl, 0, 0);
@@ -435,7 +443,7 @@ __global__ __launch_bounds__(CH == 1 ? 64 * kQ4MaxChunks : 64) void q4_direct_ke
     const h2 scale_g = {sg, sg};
     acc_g = q4_mfma(st.a[0], dequant8<false>(st.qg, scale_g), acc_g);
     acc_g = q4_mfma(st.a[1], dequant8<true>(st.qg, scale_g), acc_g);
-    if constexpr (SWIGLU) {
+    if constexpr (BOTH) {
       const _Float16 su = __builtin_bit_cast(h2, st.su)[0];
       const h2 scale_u = {su, su};
       acc_u = q4_mfma(st.a[0], dequant8<false>(st.qu, scale_u), acc_u);
@@ -470,7 +478,7 @@ __global__ __launch_bounds__(CH == 1 ? 64 * kQ4MaxChunks : 64) void q4_direct_ke
       if ((kb + kQ4Ahead) % kQ4ChunkBlocks == 0 || kb + kQ4Ahead >= kblocks) {
         tot_g = kb < kQ4ChunkBlocks ? acc_g : tot_g + acc_g;
         acc_g = f16x{};
-        if constexpr (SWIGLU) {
+        if constexpr (BOTH) {
           tot_u = kb < kQ4ChunkBlocks ? acc_u : tot_u + acc_u;
           acc_u = f16x{};
         }
@@ -497,6 +505,13 @@ __global__ __launch_bounds__(CH == 1 ? 64 * kQ4MaxChunks : 64) void q4_direct_ke
       acc_g = acc_g + part_g[c - 1][lane];
       if constexpr (SWIGLU) acc_u = acc_u + part_u[c - 1][lane];
     }
+  }
+  if constexpr (PAIR) {
+    __shared__ f16x up[64];
+    if (half) up[lane] = acc_g;
+    __syncthreads();
+    if (half) return;
+    acc_u = up[lane];
   }
 
   // D (32 x 32): lane holds column l32 and rows 8 (r / 4) + 4 hl + r % 4 -- as the tiled kernel.
@@ -525,6 +540,9 @@ void launch_q4_direct(const _Float16* x, int64_t ldx, int M, int K, const uint8_
   else if (chunks > 1)
     hipLaunchKernelGGL((q4_direct_kernel<SWIGLU, 2>), dim3((unsigned)blocks), dim3(64), 0, stream, x, ldx, M, K, w,
                        w_bytes, N, y, ldy, blocks_m, blocks);
+  else if (SWIGLU && blocks <= kQ4ChunkParallelBlocks)
+    hipLaunchKernelGGL((q4_direct_kernel<SWIGLU, SWIGLU ? 3 : 0>), dim3((unsigned)blocks), dim3(128), 0, stream, x,
+                       ldx, M, K, w, w_bytes, N, y, ldy, blocks_m, blocks);
   else
     hipLaunchKernelGGL((q4_direct_kernel<SWIGLU, 0>), dim3((unsigned)blocks), dim3(64), 0, stream, x, ldx, M,
                        K, w, w_bytes, N, y, ldy, blocks_m, blocks);
