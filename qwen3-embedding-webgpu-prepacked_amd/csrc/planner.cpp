@@ -37,9 +37,12 @@ namespace {
 // cost about three tiles that the pipeline does not hide, a workgroup's start (all launch
 // together, so their first loads queue at HBM) and end about four and a half, and a chunk of a
 // split item no more than any other entry.  Refits on other plans gave 2.2-3.3 tiles per entry
-// and 1.2-1.3 for the second workgroup; these constants measured fastest among them (16x500:
-// 37.5 us with the previous 0.75-tile entries and 1.2 factor, 35.6 us with these).
-constexpr int kEntryCost = 13;
+// and 1.2-1.3 for the second workgroup (16x500: 37.5 us with the previous 0.75-tile entries and
+// 1.2 factor, 35.6 us with 3.25-tile entries and 1.3).  Per-slot timelines of the current kernel
+// put the second workgroup at 1.6x the first per tile and 1.26x per entry; among factors 1.3-1.6
+// and entries of 2.75-3.75 tiles, 1.4 and 3.5 measured fastest (interleaved A/B: 16x500 -0.9%,
+// 4x5000 -0.5%, the other launches within 0.3%).
+constexpr int kEntryCost = 14;
 int item_cost(int ntiles) { return 4 * ntiles + kEntryCost; }
 constexpr int kSlotBase = 18;
 constexpr int kChunkExtra = 0;
@@ -50,7 +53,7 @@ constexpr int kMergeCost = 10;
 // Slot speeds, in time per unit of cost (per mille): slots cu_count..2*cu_count-1 (an XCD's
 // first 32 workgroups take one CU each) are the second workgroups.
 constexpr int64_t kFirstSlotTime = 1000;
-constexpr int64_t kSecondSlotTime = 1300;
+constexpr int64_t kSecondSlotTime = 1400;
 
 }  // namespace
 
