@@ -548,16 +548,38 @@ void launch_q4_direct(const _Float16* x, int64_t ldx, int M, int K, const uint8_
                        K, w, w_bytes, N, y, ldy, blocks_m, blocks);
 }
 
-// y = f16(part[0] + part[1] + ...), summed in chunk order (part: chunks x M x N fp32).
+// y = f16(part[0] + part[1] + ...), summed in chunk order (part: chunks x M x N fp32).  Thread =
+// four consecutive columns of row blockIdx.y (16-byte partial loads and an 8-byte store when the
+// alignment allows; the same fp32 additions either way).
 __global__ __launch_bounds__(256) void q4_reduce_kernel(const float* __restrict__ part, int chunks, int M, int N,
                                                         _Float16* __restrict__ y, int64_t ldy) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (int64_t)M * N) return;
-  const int64_t m = i / N, n = i % N;
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  const int m = blockIdx.y;
+  const int n0 = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (n0 >= N) return;
   const size_t plane = (size_t)M * (size_t)N;
-  float s = part[i];
-  for (int c = 1; c < chunks; ++c) s = s + part[(size_t)c * plane + i];
-  y[m * ldy + n] = (_Float16)s;
+  const float* p = part + (size_t)m * N + n0;
+  _Float16* yr = y + (int64_t)m * ldy + n0;
+  if ((N & 3) == 0) {  // rows, planes and this thread's columns start 16-byte aligned
+    f4 s = *reinterpret_cast<const f4*>(p);
+    for (int c = 1; c < chunks; ++c) s = s + *reinterpret_cast<const f4*>(p + (size_t)c * plane);
+    const h4 v = {(_Float16)s[0], (_Float16)s[1], (_Float16)s[2], (_Float16)s[3]};
+    if ((reinterpret_cast<uintptr_t>(yr) & 7) == 0) {
+      *reinterpret_cast<h4*>(yr) = v;
+    } else {
+      yr[0] = v[0];
+      yr[1] = v[1];
+      yr[2] = v[2];
+      yr[3] = v[3];
+    }
+  } else {
+    for (int j = 0; j < 4 && n0 + j < N; ++j) {
+      float s = p[j];
+      for (int c = 1; c < chunks; ++c) s = s + p[(size_t)c * plane + j];
+      yr[j] = (_Float16)s;
+    }
+  }
 }
 
 // Grid: 8 * ceil(tiles / 8) workgroups of 256 threads (the surplus ones exit at once), 128 x 128
@@ -597,9 +619,9 @@ hipError_t launch_q4(const _Float16* x, int64_t ldx, int M, int K, const uint8_t
     launch_q4_direct<SWIGLU>(x, ldx, M, K, w, w_bytes, N, y, ldy, stream);
   } else if (split && ws && split <= ws_bytes) {
     launch_q4_shape<SWIGLU, 1, 2>(x, ldx, M, K, w, w_bytes, N, y, ldy, stream, ws, chunks);
-    const int64_t n = (int64_t)M * N;
-    hipLaunchKernelGGL(q4_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, ws, chunks, M, N, y,
-                       ldy);
+    // one row per grid row (M < 64 * kQ4SplitTiles here), 1024 columns per workgroup
+    hipLaunchKernelGGL(q4_reduce_kernel, dim3((unsigned)((N + 1023) / 1024), (unsigned)M), dim3(256), 0, stream, ws,
+                       chunks, M, N, y, ldy);
   } else if (big_tiles < kQ4SmallLaunch) {
     launch_q4_tiled<SWIGLU, 1>(x, ldx, M, K, w, w_bytes, N, y, ldy, stream);
   } else {
