@@ -52,8 +52,9 @@ extern "C" {
  * 6: qattn_q4_matmul_swiglu; the model plan's FFN gate/up projection and SwiGLU are one launch
  * 7: qattn_run_update no longer waits for the device (two work-list images per run);
  *    qattn_debug_fail_allocs
- * 8: qattn_debug_run_timeline */
-#define QATTN_ABI_VERSION 8
+ * 8: qattn_debug_run_timeline
+ * 9: qattn_buffer_read_after, qattn_event_synchronize */
+#define QATTN_ABI_VERSION 9
 
 #define QATTN_Q_HEADS 16
 #define QATTN_KV_HEADS 8
@@ -89,12 +90,21 @@ int qattn_device_name(qattn_ctx* ctx, char* buf, size_t len, int* cu_count);
 
 /* ---- device buffers  (replaces createBuffer / createBufferWithData, device.ts:26-37, and
  *      queue.writeBuffer / mapAsync readback, model.ts:115-116,135) ----------------------- */
+typedef void* qattn_event_t; /* a HIP event (qattn_event_create, timing section below) */
 int qattn_buffer_alloc(qattn_ctx* ctx, size_t bytes, void** dptr);
 int qattn_buffer_free(qattn_ctx* ctx, void* dptr);
 /* Synchronous on the context stream. */
 int qattn_buffer_write(qattn_ctx* ctx, void* dst, size_t offset, const void* src, size_t bytes);
 int qattn_buffer_read(qattn_ctx* ctx, const void* src, size_t offset, void* dst, size_t bytes);
 int qattn_buffer_fill_u16(qattn_ctx* ctx, void* dst, uint16_t value, size_t count);
+/* The readback of one submit (the reference copies the embeddings into its readback buffer in the
+ * same submit and maps it, model.ts:133-135): copies `bytes` from src + offset to host memory dst
+ * once the work recorded before event `after` (qattn_event_record on the context stream) has
+ * finished, on a stream of the context's own for readbacks, so work enqueued on the context stream
+ * after that event (the next batch) is not waited for.  Blocks until the copy is done; safe to call
+ * from another host thread while this one enqueues. */
+int qattn_buffer_read_after(qattn_ctx* ctx, qattn_event_t after, const void* src, size_t offset,
+                            void* dst, size_t bytes);
 
 /* ---- attention operator  (replaces CausalAttentionKernel, ops.ts:318-345) ---------------- */
 typedef struct qattn_run_desc {
@@ -451,10 +461,13 @@ int qattn_gen_qkv(qattn_ctx* ctx, uint32_t config, uint32_t layer, const int32_t
                   void* v, int64_t v_row_stride, qattn_stream_t stream);
 
 /* ---- timing (hosts without a HIP runtime: Node, ctypes) ------------------------------------ */
-typedef void* qattn_event_t;
 int qattn_event_create(qattn_ctx* ctx, qattn_event_t* ev);
 int qattn_event_record(qattn_event_t ev, qattn_stream_t stream);
 int qattn_event_elapsed_ms(qattn_event_t start, qattn_event_t stop, float* ms);
+/* Blocks until the work recorded before `ev` has finished (the reference's per-submit
+ * readback, model.ts:133-135): a host that keeps several batches in
+ * flight on one stream waits for each batch's own event, not for the stream. */
+int qattn_event_synchronize(qattn_event_t ev);
 int qattn_event_destroy(qattn_event_t ev);
 
 #ifdef __cplusplus

@@ -194,8 +194,15 @@ int qattn_create(int device, qattn_ctx** out) {
     delete ctx;
     return fail(nullptr, QATTN_EHIP, "hipStreamCreate: %s", hipGetErrorString(e));
   }
+  e = hipStreamCreateWithFlags(&ctx->read_stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return fail(nullptr, QATTN_EHIP, "hipStreamCreate: %s", hipGetErrorString(e));
+  }
   e = hipGetSymbolAddress(&ctx->scratch, HIP_SYMBOL(scratch));
   if (e != hipSuccess || !ctx->scratch) {
+    (void)hipStreamDestroy(ctx->read_stream);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return fail(nullptr, QATTN_EHIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
@@ -211,6 +218,10 @@ void qattn_destroy(qattn_ctx* ctx) {
     if (ctx->stream) {
       (void)hipStreamSynchronize(ctx->stream);
       (void)hipStreamDestroy(ctx->stream);
+    }
+    if (ctx->read_stream) {
+      (void)hipStreamSynchronize(ctx->read_stream);
+      (void)hipStreamDestroy(ctx->read_stream);
     }
     if (ctx->rope) (void)hipFree(ctx->rope);
   }
@@ -273,6 +284,18 @@ int qattn_buffer_read(qattn_ctx* ctx, const void* src, size_t offset, void* dst,
   DeviceGuard g(ctx->device);
   HIP_TRY(ctx, hipMemcpyAsync(dst, static_cast<const char*>(src) + offset, bytes, hipMemcpyDeviceToHost, ctx->stream));
   HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  return QATTN_OK;
+}
+
+int qattn_buffer_read_after(qattn_ctx* ctx, qattn_event_t after, const void* src, size_t offset, void* dst,
+                            size_t bytes) {
+  if (!ctx || !after || !src || (!dst && bytes)) return fail(ctx, QATTN_EINVAL, "NULL argument");
+  DeviceGuard g(ctx->device);
+  HIP_TRY(ctx, hipStreamWaitEvent(ctx->read_stream, reinterpret_cast<hipEvent_t>(after), 0));
+  if (bytes)
+    HIP_TRY(ctx, hipMemcpyAsync(dst, static_cast<const char*>(src) + offset, bytes, hipMemcpyDeviceToHost,
+                                ctx->read_stream));
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->read_stream));
   return QATTN_OK;
 }
 
@@ -964,6 +987,12 @@ int qattn_event_elapsed_ms(qattn_event_t a, qattn_event_t b, float* ms) {
   if (!a || !b || !ms) return fail(nullptr, QATTN_EINVAL, "NULL argument");
   HIP_TRY(nullptr, hipEventSynchronize(reinterpret_cast<hipEvent_t>(b)));
   HIP_TRY(nullptr, hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(a), reinterpret_cast<hipEvent_t>(b)));
+  return QATTN_OK;
+}
+
+int qattn_event_synchronize(qattn_event_t ev) {
+  if (!ev) return fail(nullptr, QATTN_EINVAL, "event is NULL");
+  HIP_TRY(nullptr, hipEventSynchronize(reinterpret_cast<hipEvent_t>(ev)));
   return QATTN_OK;
 }
 

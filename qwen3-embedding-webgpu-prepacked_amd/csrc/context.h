@@ -13,6 +13,7 @@ struct qattn_ctx {
   int device = 0;
   int cu_count = 0;
   hipStream_t stream = nullptr;
+  hipStream_t read_stream = nullptr;  // qattn_buffer_read_after's copies (waits on events only)
   void* scratch = nullptr;  // this device's copy of the static work-list array (qattn_prefill_static)
   // RoPE table of the producer, [positions][64] (cos, sin), built for `rope_theta`; grown when a
   // longer sequence arrives (the reference builds one per plan, model.ts:76-83).

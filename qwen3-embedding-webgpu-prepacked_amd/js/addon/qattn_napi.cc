@@ -43,6 +43,7 @@ struct Buf;
 struct Run;
 struct Model;
 struct Plan;
+struct Evt;
 struct Ctx {
   qattn_ctx* ctx = nullptr;
   int refs = 1;  // the context handle's own reference
@@ -50,6 +51,16 @@ struct Ctx {
   std::set<Run*> runs;
   std::set<Model*> models;
   std::set<Plan*> plans;
+  std::set<Evt*> evts;
+  int async_busy = 0;  // synchronizeAsync / readAfterAsync waits on worker threads
+};
+// An event on the context stream (marks the end of one submitted batch).  While a readAfterAsync
+// waits on it on a worker thread, destroying it is deferred to the end of that wait.
+struct Evt {
+  Ctx* owner = nullptr;
+  qattn_event_t ev = nullptr;
+  int waiters = 0;
+  bool destroy_pending = false;
 };
 struct Buf {
   Ctx* owner = nullptr;
@@ -158,6 +169,11 @@ bool typed_bytes(napi_env env, napi_value v, void** data, size_t* bytes) {
 // Runs, then buffers, then the device context: everything still alive on `c`.
 void release_device(Ctx* c) {
   if (!c->ctx) return;
+  for (Evt* e : c->evts)
+    if (e->ev && e->waiters == 0) {
+      qattn_event_destroy(e->ev);
+      e->ev = nullptr;
+    }
   for (Plan* p : c->plans)
     if (p->plan) {
       qattn_model_plan_destroy(p->plan);
@@ -241,6 +257,10 @@ napi_value DestroyContext(napi_env env, napi_callback_info info) {
   if (!args_of(env, info, 1, argv)) return nullptr;
   Ctx* c = get_external<Ctx>(env, argv[0], "context");
   if (!c) return nullptr;
+  if (c->async_busy > 0) {
+    napi_throw_error(env, nullptr, "context has asynchronous waits in flight; await them first");
+    return nullptr;
+  }
   release_device(c);
   return undefined(env);
 }
@@ -1103,6 +1123,7 @@ napi_value Synchronize(napi_env env, napi_callback_info info) {
 struct SyncWork {
   napi_async_work work = nullptr;
   napi_deferred deferred = nullptr;
+  Ctx* owner = nullptr;
   qattn_ctx* ctx = nullptr;
   int rc = 0;
   std::string msg;
@@ -1124,6 +1145,8 @@ void sync_complete(napi_env env, napi_status, void* data) {
     napi_reject_deferred(env, w->deferred, e);
   }
   napi_delete_async_work(env, w->work);
+  --w->owner->async_busy;
+  unref(w->owner);
   delete w;
 }
 napi_value SynchronizeAsync(napi_env env, napi_callback_info info) {
@@ -1132,11 +1155,171 @@ napi_value SynchronizeAsync(napi_env env, napi_callback_info info) {
   Ctx* c = live_ctx(env, argv[0]);
   if (!c) return nullptr;
   auto* w = new SyncWork();
+  w->owner = c;
   w->ctx = c->ctx;
+  ++c->refs;
+  ++c->async_busy;
   napi_value promise, name;
   NAPI_OK(env, napi_create_promise(env, &w->deferred, &promise));
   NAPI_OK(env, napi_create_string_utf8(env, "qattn.synchronize", NAPI_AUTO_LENGTH, &name));
   NAPI_OK(env, napi_create_async_work(env, nullptr, name, sync_execute, sync_complete, w, &w->work));
+  NAPI_OK(env, napi_queue_async_work(env, w->work));
+  return promise;
+}
+
+// createEvent(ctx) / recordEvent(ev) (on the context stream) / destroyEvent(ev).
+void finalize_evt(napi_env, void* data, void*) {
+  auto* e = static_cast<Evt*>(data);
+  Ctx* c = e->owner;
+  if (e->ev && c->ctx) qattn_event_destroy(e->ev);
+  c->evts.erase(e);
+  delete e;
+  unref(c);
+}
+napi_value CreateEvent(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!args_of(env, info, 1, argv)) return nullptr;
+  Ctx* c = live_ctx(env, argv[0]);
+  if (!c) return nullptr;
+  qattn_event_t ev = nullptr;
+  int rc = qattn_event_create(c->ctx, &ev);
+  if (rc) return throw_qattn(env, rc, c->ctx);
+  auto* e = new Evt{c, ev};
+  c->evts.insert(e);
+  ++c->refs;
+  napi_value out;
+  NAPI_OK(env, napi_create_external(env, e, finalize_evt, nullptr, &out));
+  return out;
+}
+Evt* live_evt(napi_env env, napi_value v) {
+  Evt* e = get_external<Evt>(env, v, "event");
+  if (e && (!e->ev || e->destroy_pending || !e->owner->ctx)) {
+    napi_throw_error(env, nullptr, "event was destroyed");
+    return nullptr;
+  }
+  return e;
+}
+napi_value RecordEvent(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!args_of(env, info, 1, argv)) return nullptr;
+  Evt* e = live_evt(env, argv[0]);
+  if (!e) return nullptr;
+  int rc = qattn_event_record(e->ev, qattn_stream(e->owner->ctx));
+  if (rc) return throw_qattn(env, rc, e->owner->ctx);
+  return undefined(env);
+}
+napi_value DestroyEvent(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!args_of(env, info, 1, argv)) return nullptr;
+  Evt* e = get_external<Evt>(env, argv[0], "event");
+  if (!e) return nullptr;
+  if (e->waiters > 0) {
+    e->destroy_pending = true;
+  } else if (e->ev && e->owner->ctx) {
+    qattn_event_destroy(e->ev);
+    e->ev = nullptr;
+  }
+  return undefined(env);
+}
+
+// readAfterAsync(buf, ev, dst) -> Promise<dst>: the readback of one submit -- dst (a typed array,
+// at most the buffer's size) receives the buffer's first dst.byteLength bytes once the work
+// recorded before ev has finished, copied on the context's readback stream by a worker thread
+// (qattn_buffer_read_after), so batches enqueued after ev are not waited for.  The buffer, the
+// event and dst stay referenced until the promise settles.
+struct ReadWork {
+  napi_async_work work = nullptr;
+  napi_deferred deferred = nullptr;
+  napi_ref buf_ref = nullptr, evt_ref = nullptr, dst_ref = nullptr;
+  Evt* evt = nullptr;
+  qattn_ctx* ctx = nullptr;
+  const void* src = nullptr;
+  void* dst = nullptr;
+  size_t bytes = 0;
+  int rc = 0;
+  std::string msg;
+};
+void read_execute(napi_env, void* data) {
+  auto* w = static_cast<ReadWork*>(data);
+  w->rc = qattn_buffer_read_after(w->ctx, w->evt->ev, w->src, 0, w->dst, w->bytes);
+  if (w->rc) w->msg = qattn_last_error(w->ctx);
+}
+void read_complete(napi_env env, napi_status, void* data) {
+  auto* w = static_cast<ReadWork*>(data);
+  Evt* e = w->evt;
+  if (--e->waiters == 0 && e->destroy_pending && e->ev && e->owner->ctx) {
+    qattn_event_destroy(e->ev);
+    e->ev = nullptr;
+  }
+  if (w->rc == 0) {
+    napi_value dst;
+    napi_get_reference_value(env, w->dst_ref, &dst);
+    napi_resolve_deferred(env, w->deferred, dst);
+  } else {
+    napi_value m, err;
+    std::string s = "qattn error " + std::to_string(w->rc) + ": " + w->msg;
+    napi_create_string_utf8(env, s.c_str(), NAPI_AUTO_LENGTH, &m);
+    napi_create_error(env, nullptr, m, &err);
+    napi_reject_deferred(env, w->deferred, err);
+  }
+  napi_delete_reference(env, w->buf_ref);
+  napi_delete_reference(env, w->evt_ref);
+  napi_delete_reference(env, w->dst_ref);
+  napi_delete_async_work(env, w->work);
+  --e->owner->async_busy;
+  unref(e->owner);
+  delete w;
+}
+napi_value ReadAfterAsync(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  if (!args_of(env, info, 3, argv)) return nullptr;
+  Buf* b = live_buf(env, argv[0]);
+  if (!b) return nullptr;
+  Evt* e = live_evt(env, argv[1]);
+  if (!e) return nullptr;
+  if (e->owner != b->owner) {
+    napi_throw_error(env, nullptr, "buffer and event belong to different contexts");
+    return nullptr;
+  }
+  bool is_typed = false;
+  napi_is_typedarray(env, argv[2], &is_typed);
+  if (!is_typed) {
+    napi_throw_type_error(env, nullptr, "dst must be a typed array");
+    return nullptr;
+  }
+  napi_typedarray_type type;
+  size_t length = 0, byte_offset = 0;
+  void* data = nullptr;
+  napi_value ab;
+  NAPI_OK(env, napi_get_typedarray_info(env, argv[2], &type, &length, &data, &ab, &byte_offset));
+  size_t elem = 1;
+  switch (type) {
+    case napi_int16_array: case napi_uint16_array: elem = 2; break;
+    case napi_int32_array: case napi_uint32_array: case napi_float32_array: elem = 4; break;
+    case napi_float64_array: case napi_bigint64_array: case napi_biguint64_array: elem = 8; break;
+    default: elem = 1;
+  }
+  const size_t bytes = length * elem;
+  if (bytes > b->bytes) {
+    napi_throw_range_error(env, nullptr, "dst is larger than the buffer");
+    return nullptr;
+  }
+  auto* w = new ReadWork();
+  w->evt = e;
+  w->ctx = b->owner->ctx;
+  w->src = b->ptr;
+  w->dst = data;
+  w->bytes = bytes;
+  NAPI_OK(env, napi_create_reference(env, argv[0], 1, &w->buf_ref));
+  NAPI_OK(env, napi_create_reference(env, argv[1], 1, &w->evt_ref));
+  NAPI_OK(env, napi_create_reference(env, argv[2], 1, &w->dst_ref));
+  ++e->waiters;
+  ++b->owner->refs;  // the context outlives the wait
+  ++b->owner->async_busy;
+  napi_value promise, name;
+  NAPI_OK(env, napi_create_promise(env, &w->deferred, &promise));
+  NAPI_OK(env, napi_create_string_utf8(env, "qattn.readAfter", NAPI_AUTO_LENGTH, &name));
+  NAPI_OK(env, napi_create_async_work(env, nullptr, name, read_execute, read_complete, w, &w->work));
   NAPI_OK(env, napi_queue_async_work(env, w->work));
   return promise;
 }
@@ -1167,6 +1350,8 @@ napi_value Init(napi_env env, napi_value exports) {
       {"createModel", CreateModel},   {"destroyModel", DestroyModel},
       {"createModelPlan", CreateModelPlan}, {"destroyModelPlan", DestroyModelPlan},
       {"runModelPlan", RunModelPlan}, {"profileModelPlan", ProfileModelPlan},
+      {"createEvent", CreateEvent},   {"recordEvent", RecordEvent},
+      {"destroyEvent", DestroyEvent}, {"readAfterAsync", ReadAfterAsync},
   };
   for (const Fn& f : fns) {
     napi_value fn;

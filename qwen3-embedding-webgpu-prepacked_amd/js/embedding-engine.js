@@ -13,8 +13,15 @@
 // for padding.  Runtimes without that property get exactly the reference's padded layout.
 // Plans are cached per `${batch}:${sequence}` (ee:70-75) in both modes, sequence being the
 // longest request.
+//
+// Pipelining.  The reference awaits each micro-batch's run before packing the next (ee:76-78).
+// A plan that also offers enqueue(ids, lengths) -> ticket and complete(ticket) -> Promise of the
+// embeddings (HipQwen3Plan) gets up to MAX_IN_FLIGHT batches submitted at once: while one runs on
+// the GPU, the next is packed and enqueued.  Batches still resolve in order, one batch's failure
+// rejects only its requests, and plans with run() alone are run as in the reference.
 
 const MAX_BATCH = 16;
+const MAX_IN_FLIGHT = 2;
 
 function packPadded(tokenLists, eosToken) {
   const sequence = Math.max.apply(null, tokenLists.map((t) => t.length));
@@ -84,8 +91,22 @@ class Qwen3EmbeddingEngine {
   async flush() {
     if (this.flushing) return;
     this.flushing = true;
+    const inFlight = [];
+    // A failed batch rejects every request in it (ee:79-81); later batches still run.
+    const finish = async ({ requests, plan, ticket }) => {
+      try {
+        const embeddings = await plan.complete(ticket);
+        requests.forEach((request, index) => request.resolve(embeddings[index]));
+      } catch (error) {
+        requests.forEach((request) => request.reject(error));
+      }
+    };
     try {
-      while (this.pending.length > 0) {
+      while (this.pending.length > 0 || inFlight.length > 0) {
+        if (this.pending.length === 0 || inFlight.length >= MAX_IN_FLIGHT) {
+          await finish(inFlight.shift());
+          continue;
+        }
         const requests = this.pending.splice(0, this.maxBatchSize);
         const tokenLists = requests.map((request) => request.tokens);
         const packed = this.runtime.packing === 'varlen' ? packVarlen(tokenLists) : packPadded(tokenLists, this.eosToken);
@@ -96,10 +117,15 @@ class Qwen3EmbeddingEngine {
             plan = this.runtime.createPlan(requests.length, packed.sequence);
             this.plans.set(key, plan);
           }
+          if (typeof plan.enqueue === 'function' && typeof plan.complete === 'function') {
+            // submitted; the next batch is packed while this one runs
+            inFlight.push({ requests, plan, ticket: plan.enqueue(packed.ids, packed.lengths) });
+            continue;
+          }
+          while (inFlight.length > 0) await finish(inFlight.shift());
           const embeddings = await plan.run(packed.ids, packed.lengths);
           requests.forEach((request, index) => request.resolve(embeddings[index]));
         } catch (error) {
-          // A failed batch rejects every request in it (ee:79-81); later batches still run.
           requests.forEach((request) => request.reject(error));
         }
       }
@@ -110,4 +136,4 @@ class Qwen3EmbeddingEngine {
   }
 }
 
-module.exports = { Qwen3EmbeddingEngine, packPadded, packVarlen, cuSeqlensOf, MAX_BATCH };
+module.exports = { Qwen3EmbeddingEngine, packPadded, packVarlen, cuSeqlensOf, MAX_BATCH, MAX_IN_FLIGHT };

@@ -8,6 +8,10 @@ export type TokenizerLike = (text: string) => TokenizerResult;
 
 export interface EmbeddingPlan {
   run(ids: Uint32Array, lengths: Uint32Array): Promise<Float32Array[]>;
+  /** Optional split of run(): a plan that has both gets up to two batches in flight from the
+   *  engine (the next is packed and enqueued while one runs); results still resolve in order. */
+  enqueue?(ids: Uint32Array, lengths: Uint32Array): unknown;
+  complete?(ticket: unknown): Promise<Float32Array[]>;
 }
 export interface EmbeddingRuntime {
   /** 'varlen': the engine packs requests back to back (ids.length === sum(lengths)). */
@@ -155,9 +159,14 @@ export class HipQwen3Model {
   createPlan(batch: number, sequence: number): HipQwen3Plan;
   destroy(): void;
 }
+export interface HipQwen3Ticket { readonly n: number; readonly tokens: number }
 export class HipQwen3Plan implements EmbeddingPlan {
   /** Packed token ids (lengths[i] per request) -> one L2-normalised Float32Array(1024) per request. */
   run(ids: Uint32Array | Int32Array, lengths: Uint32Array | number[]): Promise<Float32Array[]>;
+  /** Submits one batch and returns at once (at most two of this plan in flight). */
+  enqueue(ids: Uint32Array | Int32Array, lengths: Uint32Array | number[]): HipQwen3Ticket;
+  /** The embeddings of an enqueued batch, once its own work is done (later batches not waited for). */
+  complete(ticket: HipQwen3Ticket): Promise<Float32Array[]>;
   /** One run with each stage timed: total ms per stage over all layers. */
   profile(ids: Uint32Array | Int32Array, lengths: Uint32Array | number[]): Record<ModelStage, number>;
   readonly timing: { hostMs: number; totalMs: number; tokens: number } | null;

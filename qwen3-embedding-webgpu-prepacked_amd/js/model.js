@@ -9,6 +9,8 @@
 //                                           `sequence` tokens each (model.ts:273)
 //   plan.run(ids, lengths)                  packed token ids -> one L2-normalised 1024-float
 //                                           embedding per request (model.ts:113-139)
+//   plan.enqueue(ids, lengths) -> ticket    the same run, submitted; plan.complete(ticket) resolves
+//                                           to its embeddings (two submits of a plan in flight)
 //   plan.profile(ids, lengths)              stage totals in ms (model.ts:141-182)
 //   new HipQwen3Runtime({ model | prepacked, context })   EmbeddingRuntime for Qwen3EmbeddingEngine
 //
@@ -117,28 +119,59 @@ class HipQwen3Plan {
     this.sequence = sequence;
     const ctx = model.context;
     this.handle = ctx.addon.createModelPlan(model.handle, batch * sequence, batch);
-    this.out = ctx.alloc(batch * HIDDEN * 4);
+    // Two output buffers, each with the event that ends its submit, so a second batch can be
+    // enqueued while the first runs (the reference's readback buffer, model.ts:90-95, 133-135).
+    this.slots = [0, 1].map(() => ({ out: ctx.alloc(batch * HIDDEN * 4), event: ctx.addon.createEvent(ctx.handle), busy: false }));
+    this.next = 0;
     this.timing = null;
   }
 
   // ids: the requests' token ids packed back to back (Uint32Array / Int32Array), lengths[i] tokens
   // for request i; resolves to one Float32Array(1024) per request.
   async run(ids, lengths) {
+    return this.complete(this.enqueue(ids, lengths));
+  }
+
+  // Submits one batch on the context stream and returns at once; at most two per plan may be in
+  // flight (complete() frees a slot).  Batches run in submission order.
+  enqueue(ids, lengths) {
     const cu = this.check(ids, lengths);
+    const slot = this.slots[this.next];
+    if (slot.busy) throw new Error('two batches of this plan are already in flight');
     const start = process.hrtime.bigint();
-    const ctx = this.model.context;
-    ctx.addon.runModelPlan(this.handle, ids, cu, this.out.handle);
-    const enqueued = process.hrtime.bigint();
-    await ctx.synchronizeAsync();
+    const addon = this.model.context.addon;
+    addon.runModelPlan(this.handle, ids, cu, slot.out.handle);
+    addon.recordEvent(slot.event);
+    slot.busy = true;
+    this.next ^= 1;
+    return { slot, n: lengths.length, tokens: cu[cu.length - 1], start, enqueued: process.hrtime.bigint() };
+  }
+
+  // Resolves to the embeddings of an enqueued batch once its own work is done (a later batch is
+  // not waited for).
+  async complete(ticket) {
+    const flat = new Float32Array(ticket.n * HIDDEN);
+    try {
+      await this.model.context.addon.readAfterAsync(ticket.slot.out.handle, ticket.slot.event, flat);
+    } finally {
+      ticket.slot.busy = false;
+    }
     const done = process.hrtime.bigint();
-    this.timing = { hostMs: Number(enqueued - start) / 1e6, totalMs: Number(done - start) / 1e6, tokens: cu[cu.length - 1] };
-    return this.read(lengths.length);
+    this.timing = {
+      hostMs: Number(ticket.enqueued - ticket.start) / 1e6,
+      totalMs: Number(done - ticket.start) / 1e6,
+      tokens: ticket.tokens,
+    };
+    const out = [];
+    for (let i = 0; i < ticket.n; i += 1) out.push(flat.subarray(i * HIDDEN, (i + 1) * HIDDEN));
+    return out;
   }
 
   // One run with every stage timed: { stage name: ms over all layers } (model.ts:141-182 names).
   profile(ids, lengths) {
+    if (this.slots.some((slot) => slot.busy)) throw new Error('profile() while batches of this plan are in flight');
     const cu = this.check(ids, lengths);
-    return this.model.context.addon.profileModelPlan(this.handle, ids, cu, this.out.handle);
+    return this.model.context.addon.profileModelPlan(this.handle, ids, cu, this.slots[0].out.handle);
   }
 
   check(ids, lengths) {
@@ -150,17 +183,16 @@ class HipQwen3Plan {
     return cu;
   }
 
-  read(n) {
-    const flat = this.out.read(new Float32Array(n * HIDDEN));
-    const out = [];
-    for (let i = 0; i < n; i += 1) out.push(flat.subarray(i * HIDDEN, (i + 1) * HIDDEN));
-    return out;
-  }
-
   destroy() {
-    if (this.handle) this.model.context.addon.destroyModelPlan(this.handle);
+    if (this.slots.some((slot) => slot.busy)) throw new Error('destroy() while batches of this plan are in flight');
+    const addon = this.model.context.addon;
+    if (this.handle) addon.destroyModelPlan(this.handle);
     this.handle = null;
-    this.out.destroy();
+    for (const slot of this.slots) {
+      addon.destroyEvent(slot.event);
+      slot.out.destroy();
+    }
+    this.slots = [];
   }
 }
 

@@ -115,6 +115,7 @@ def lib():
         "qattn_buffer_free": (ctypes.c_int, [vp, vp]),
         "qattn_buffer_write": (ctypes.c_int, [vp, vp, sz, vp, sz]),
         "qattn_buffer_read": (ctypes.c_int, [vp, vp, sz, vp, sz]),
+        "qattn_buffer_read_after": (ctypes.c_int, [vp, vp, vp, sz, vp, sz]),
         "qattn_buffer_fill_u16": (ctypes.c_int, [vp, vp, ctypes.c_uint16, sz]),
         "qattn_run_create": (ctypes.c_int, [vp, ctypes.POINTER(RunDesc), pvp]),
         "qattn_run_encode": (ctypes.c_int, [vp, vp]),
@@ -148,6 +149,7 @@ def lib():
         "qattn_event_create": (ctypes.c_int, [vp, pvp]),
         "qattn_event_record": (ctypes.c_int, [vp, vp]),
         "qattn_event_elapsed_ms": (ctypes.c_int, [vp, vp, ctypes.POINTER(ctypes.c_float)]),
+        "qattn_event_synchronize": (ctypes.c_int, [vp]),
         "qattn_event_destroy": (ctypes.c_int, [vp]),
         "qattn_embed_q6k": (ctypes.c_int, [vp, vp, i64, vp, i64, i32, vp, i64, vp]),
         "qattn_rmsnorm": (ctypes.c_int, [vp, vp, i64, vp, i64, vp, vp, i64, i64, i32, ctypes.c_double, vp]),
@@ -240,6 +242,15 @@ class Buffer:
                self.ctx.handle)
         return out
 
+    def read_after(self, event, dtype, shape, offset=0):
+        """The buffer's contents once the work recorded before `event` has finished, without
+        waiting for work enqueued after it (qattn_buffer_read_after)."""
+        out = np.empty(shape, dtype=dtype)
+        assert offset + out.nbytes <= self.nbytes
+        _check(lib().qattn_buffer_read_after(self.ctx.handle, event.handle, self.ptr, offset, _np_ptr(out),
+                                             out.nbytes), self.ctx.handle)
+        return out
+
     def fill_u16(self, value, count=None):
         count = self.nbytes // 2 if count is None else count
         _check(lib().qattn_buffer_fill_u16(self.ctx.handle, self.ptr, value, count), self.ctx.handle)
@@ -315,6 +326,9 @@ class Event:
         ms = ctypes.c_float()
         _check(lib().qattn_event_elapsed_ms(self.handle, later.handle, ctypes.byref(ms)))
         return ms.value
+
+    def synchronize(self):
+        _check(lib().qattn_event_synchronize(self.handle))
 
     def destroy(self):
         if self.handle:

@@ -110,6 +110,44 @@ test('a failing createPlan rejects its batch instead of leaving it pending', asy
   await assert.rejects(engine.embed('x'), /out of memory/);
 });
 
+test('a plan with enqueue/complete gets the next batch submitted while one runs; batches resolve in order', async () => {
+  const events = [];
+  let inFlight = 0;
+  let maxInFlight = 0;
+  const runtime = {
+    packing: 'varlen',
+    createPlan(batch) {
+      return {
+        enqueue(ids, lengths) {
+          inFlight += 1;
+          maxInFlight = Math.max(maxInFlight, inFlight);
+          events.push(`enqueue ${ids[0]}`);
+          return { first: ids[0], n: lengths.length };
+        },
+        async complete(ticket) {
+          await new Promise((r) => setTimeout(r, 5));
+          inFlight -= 1;
+          events.push(`complete ${ticket.first}`);
+          if (ticket.first === 9) throw new Error('device lost');
+          return Array.from({ length: ticket.n }, (_, i) => new Float32Array([ticket.first + i]));
+        },
+        async run() { throw new Error('run() must not be used when enqueue/complete exist'); },
+      };
+    },
+  };
+  const tokenizer = (text) => ({ input_ids: { tolist: () => [[Number(text)]] } });
+  const engine = new Qwen3EmbeddingEngine(runtime, tokenizer, 4, 0, 0);
+  // 14 requests: batches [1..4] [5..8] [9..12] [13, 14]; the third batch fails
+  const settled = await Promise.allSettled(Array.from({ length: 14 }, (_, i) => engine.embed(String(i + 1))));
+  assert.strictEqual(maxInFlight, 2);
+  assert.deepStrictEqual(events, ['enqueue 1', 'enqueue 5', 'complete 1', 'enqueue 9', 'complete 5', 'enqueue 13',
+    'complete 9', 'complete 13']);
+  settled.forEach((r, i) => {
+    if (i >= 8 && i < 12) assert.strictEqual(r.status, 'rejected');
+    else assert.strictEqual(r.value[0], i + 1);
+  });
+});
+
 test('maxBatchSize outside 1..16 throws (reference ee:35)', () => {
   assert.throws(() => new Qwen3EmbeddingEngine({}, () => null, 0), /between 1 and 16/);
   assert.throws(() => new Qwen3EmbeddingEngine({}, () => null, 17), /between 1 and 16/);
@@ -134,7 +172,7 @@ test('packVarlen / cuSeqlensOf offsets', () => {
 
 test('N-API addon loads; host-side planning and validation work without a GPU', () => {
   const addon = loadAddon();
-  assert.strictEqual(addon.abiVersion(), 8);
+  assert.strictEqual(addon.abiVersion(), 9);
   const plan = addon.planDescribe({ q: 1, k: 1, v: 1, o: 1, cuSeqlens: new Int32Array([0, 50, 550]) });
   assert.strictEqual(plan.info.tokens, 550);
   assert.strictEqual(plan.info.pairs, 1275 + 125250);

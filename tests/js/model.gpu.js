@@ -28,6 +28,17 @@ async function main() {
   const alone = await engine.embed(lists[1].join(','));
   assert.ok(alone.every((x, i) => x === outs[1][i]), 'a request alone differs from the same request in a batch');
 
+  // 40 requests at once: micro-batches of 16, 16 and 8 with two submitted at a time (the next one
+  // packed and enqueued while the previous runs); each embedding equals the request's own
+  // single-request embedding bit for bit, so batches in flight do not disturb one another.
+  const many = Array.from({ length: 40 }, (_, r) => lists[r % lists.length].slice(0, 2 + ((r * 37) % (lists[r % lists.length].length - 1))));
+  many.forEach((ids) => { ids[ids.length - 1] = eos; });
+  const manyOut = await Promise.all(many.map((ids) => engine.embed(ids.join(','))));
+  for (let r = 0; r < many.length; r += 1) {
+    const single = await engine.embed(many[r].join(','));
+    assert.ok(single.every((x, i) => x === manyOut[r][i]), `request ${r}: pipelined batch differs from the request alone`);
+  }
+
   const plan = runtime.model.createPlan(2, 256);
   const ids = Uint32Array.from(lists[0].concat(lists[1]));
   const stages = plan.profile(ids, [lists[0].length, lists[1].length]);

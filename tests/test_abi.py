@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol(qattn):
 
 
 def test_abi_version(qattn):
-    assert qattn.lib().qattn_abi_version() == 8
+    assert qattn.lib().qattn_abi_version() == 9
 
 
 def test_create_without_gpu_fails_cleanly(qattn):

@@ -65,7 +65,7 @@ def test_node_model_path(tmp_path):
 @pytest.mark.skipif(shutil.which("node") is None, reason="node is not installed")
 def test_engine_benchmark_script_runs():
     """js/bench-engine.js (the engine's end-to-end timing on a synthetic model of the real
-    shapes) at 2 layers and one timed batch: both workloads report, with unit-norm embeddings."""
+    shapes) at 2 layers and one timed round: every workload reports, with unit-norm embeddings."""
     import json
     script = os.path.join(HERE, "..", "qwen3-embedding-webgpu-prepacked_amd", "js", "bench-engine.js")
     r = subprocess.run(["node", script, "2", "1"],
@@ -73,5 +73,7 @@ def test_engine_benchmark_script_runs():
     print(r.stdout, r.stderr[-2000:])
     assert r.returncode == 0, r.stdout + r.stderr
     lines = [json.loads(l) for l in r.stdout.splitlines() if l.startswith("{")]
-    assert [l["workload"] for l in lines] == ["16x500", "1x5000"]
+    assert [l["workload"] for l in lines] == ["16x500", "64x500", "1x5000"]
     assert all(l["embeddings_unit_norm"] and l["requests_per_s"] > 0 for l in lines)
+    # 64 requests: four micro-batches, each after the first enqueued while the one before it ran
+    assert lines[1]["micro_batches"] == 4 and lines[1]["enqueued_while_previous_running"] == 3
