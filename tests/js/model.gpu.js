@@ -49,6 +49,16 @@ async function main() {
   const [e0] = await plan.run(Uint32Array.from(lists[1]), [lists[1].length]);
   assert.ok(e0.every((x, i) => x === outs[1][i]), 'plan.run differs from the engine');
   plan.destroy();
+
+  // A plan or context with a readback in flight refuses to be destroyed until it settles.
+  const small = runtime.model.createPlan(1, 16);
+  const ticket = small.enqueue(Uint32Array.from([1, 2, eos]), [3]);
+  const pending = small.complete(ticket);
+  assert.throws(() => small.destroy(), /in flight/);
+  assert.throws(() => runtime.context.addon.destroyContext(runtime.context.handle), /in flight/);
+  const [tiny] = await pending;
+  assert.ok(Math.abs(Math.hypot(...tiny) - 1) < 1e-3);
+  small.destroy();
   runtime.destroy();
   console.log(JSON.stringify({ ok: true, requests: outs.length, stages }));
 }
