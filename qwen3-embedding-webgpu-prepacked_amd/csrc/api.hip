@@ -33,7 +33,8 @@ hipError_t launch_fill_normal(half_t* dst, int64_t rows, int64_t row_elems, int6
 hipError_t launch_fill_token_rows(half_t* dst, const int32_t* ids, int64_t rows, int64_t row_elems,
                                   int64_t row_stride, uint64_t seed, hipStream_t stream);
 hipError_t launch_q4_matmul(const half_t* x, int64_t ldx, int M, int K, const uint8_t* w, uint32_t w_bytes, int N,
-                            half_t* y, int64_t ldy, hipStream_t stream, float* ws, size_t ws_bytes);
+                            half_t* y, int64_t ldy, hipStream_t stream, float* ws, size_t ws_bytes,
+                            const RowNorm* norm, bool* normed);
 hipError_t launch_q4_matmul_swiglu(const half_t* x, int64_t ldx, int M, int K, const uint8_t* w, uint32_t w_bytes,
                                    int n_inter, half_t* y, int64_t ldy, hipStream_t stream);
 hipError_t launch_pool_last_l2(const half_t* x, int64_t row_stride, int width, const int32_t* cu_seqlens,
@@ -873,13 +874,15 @@ namespace qattn {
 // qattn_q4_matmul with an optional split workspace (the model plan's): launches with few tiles
 // split their K chunks over workgroups when ws holds q4_split_bytes.
 int q4_matmul_ws(qattn_ctx* ctx, const void* x, int64_t ldx, int32_t M, int32_t K, const void* w, int64_t w_bytes,
-                 int32_t N, void* y, int64_t ldy, qattn_stream_t stream, float* ws, size_t ws_bytes) {
+                 int32_t N, void* y, int64_t ldy, qattn_stream_t stream, float* ws, size_t ws_bytes,
+                 const RowNorm* norm, bool* normed) {
+  if (normed) *normed = false;
   const int rc = check_q4_args(ctx, x, ldx, M, K, w, w_bytes, N, N, y, ldy);
   if (rc != QATTN_OK) return rc;
   DeviceGuard g(ctx->device);
   HIP_TRY(ctx, launch_q4_matmul(static_cast<const half_t*>(x), ldx, M, K, static_cast<const uint8_t*>(w),
                                 (uint32_t)w_bytes, N, static_cast<half_t*>(y), ldy, pick_stream(ctx, stream), ws,
-                                ws_bytes));
+                                ws_bytes, norm, normed));
   return QATTN_OK;
 }
 }  // namespace qattn

@@ -60,9 +60,13 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // Host cu_seqlens: nseq in [1, QATTN_MAX_SEQS], cu[0] = 0, non-decreasing.
 int validate_cu(qattn_ctx* ctx, const int32_t* cu, int32_t nseq);
 
+struct RowNorm;  // model_ops.h
 // qattn_q4_matmul with an optional fp32 workspace for the split launch of small projections
-// (api.hip; the model plan passes its own).
+// (api.hip; the model plan passes its own).  With `norm`, a split launch also runs that residual
+// add + RMSNorm on its output straight from the partial sums (and does not write y); *normed
+// says whether it did, or the caller still has to.
 int q4_matmul_ws(qattn_ctx* ctx, const void* x, int64_t ldx, int32_t M, int32_t K, const void* w, int64_t w_bytes,
-                 int32_t N, void* y, int64_t ldy, qattn_stream_t stream, float* ws, size_t ws_bytes);
+                 int32_t N, void* y, int64_t ldy, qattn_stream_t stream, float* ws, size_t ws_bytes,
+                 const RowNorm* norm = nullptr, bool* normed = nullptr);
 
 }  // namespace qattn

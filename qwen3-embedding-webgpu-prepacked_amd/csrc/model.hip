@@ -255,13 +255,19 @@ int enqueue(qattn_model_plan* p, const int32_t* cu, int32_t nseq, float* out, in
                                      w.attn_k_norm, d.eps, d.rope_theta, s));
     STAGE_TRY(qattn_run_encode(p->run, s));
     end();
+    // A split projection (small batches) runs the residual add + RMSNorm that follows it straight
+    // from its partial sums; its time then falls in the projection's stage.
+    const RowNorm ffn_in{static_cast<half_t*>(p->x), kHidden, w.ffn_norm, static_cast<half_t*>(p->normalized),
+                         kHidden, (float)d.eps};
+    bool normed = false;
     begin(QATTN_STAGE_ATTENTION_OUTPUT);
     STAGE_TRY(q4_matmul_ws(ctx, p->attn, kQWidth, (int32_t)T, kQWidth, w.attn_output, w.attn_output_bytes, kHidden,
-                           p->delta, kHidden, s, p->gemm_ws, p->gemm_ws_bytes));
+                           p->delta, kHidden, s, p->gemm_ws, p->gemm_ws_bytes, &ffn_in, &normed));
     end();
     begin(QATTN_STAGE_POST_ATTENTION_NORM);
-    STAGE_TRY(qattn_rmsnorm(ctx, p->x, kHidden, p->delta, kHidden, w.ffn_norm, p->normalized, kHidden, T, kHidden,
-                            d.eps, s));
+    if (!normed)
+      STAGE_TRY(qattn_rmsnorm(ctx, p->x, kHidden, p->delta, kHidden, w.ffn_norm, p->normalized, kHidden, T, kHidden,
+                              d.eps, s));
     end();
     // The gate/up projection and SwiGLU are one launch (no [T][6144] intermediate); its time is
     // the ffn_up_gate stage and the swiglu stage stays empty.
@@ -271,13 +277,16 @@ int enqueue(qattn_model_plan* p, const int32_t* cu, int32_t nseq, float* out, in
     end();
     begin(QATTN_STAGE_SWIGLU);
     end();
+    const RowNorm next_in{static_cast<half_t*>(p->x), kHidden, next_norm, static_cast<half_t*>(p->normalized),
+                          kHidden, (float)d.eps};
     begin(QATTN_STAGE_FFN_DOWN);
     STAGE_TRY(q4_matmul_ws(ctx, p->ffn, kInter, (int32_t)T, kInter, w.ffn_down, w.ffn_down_bytes, kHidden, p->delta,
-                           kHidden, s, p->gemm_ws, p->gemm_ws_bytes));
+                           kHidden, s, p->gemm_ws, p->gemm_ws_bytes, &next_in, &normed));
     end();
     begin(QATTN_STAGE_POST_FFN_NORM);
-    STAGE_TRY(qattn_rmsnorm(ctx, p->x, kHidden, p->delta, kHidden, next_norm, p->normalized, kHidden, T, kHidden,
-                            d.eps, s));
+    if (!normed)
+      STAGE_TRY(qattn_rmsnorm(ctx, p->x, kHidden, p->delta, kHidden, next_norm, p->normalized, kHidden, T, kHidden,
+                              d.eps, s));
     end();
   }
   begin(QATTN_STAGE_POOL);

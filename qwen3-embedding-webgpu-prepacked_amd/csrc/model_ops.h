@@ -14,6 +14,21 @@ constexpr int kRmsMaxWidth = 4096;    // rmsnorm_kernel: columns per row (one wa
 // ids outside [0, vocab) give zero rows.
 hipError_t launch_embed_q6k(const int32_t* ids, int64_t tokens, const uint8_t* table, int64_t vocab, int width,
                             half_t* out, int64_t out_stride, hipStream_t stream);
+// The residual add + RMSNorm that follows a projection, with the projection's output as the
+// residual (launch_rmsnorm's other arguments).
+struct RowNorm {
+  half_t* x;
+  int64_t x_stride;
+  const float* weight;
+  half_t* out;
+  int64_t out_stride;
+  float eps;
+};
+// RowNorm on a projection's split-K partial sums (part: chunks x rows x width fp32, width a
+// multiple of 8 and <= kRmsMaxWidth, 16-byte aligned rows): bit for bit the projection's output
+// followed by launch_rmsnorm, without writing that output.
+hipError_t launch_reduce_rmsnorm(const float* part, int chunks, int rows, int width, const RowNorm& norm,
+                                 hipStream_t stream);
 // Residual add (residual may be NULL) + RMSNorm of `rows` rows of `width` (multiple of 8, <= kRmsMaxWidth).
 hipError_t launch_rmsnorm(half_t* x, const half_t* residual, const float* weight, half_t* out, int64_t rows,
                           int width, int64_t x_stride, int64_t r_stride, int64_t out_stride, float eps,

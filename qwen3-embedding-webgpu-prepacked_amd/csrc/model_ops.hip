@@ -56,15 +56,12 @@ __global__ __launch_bounds__(256) void embed_q6k_kernel(const int32_t* ids, int6
 // One wavefront per row; lane l owns columns 8l + 512j.  With a residual: v = f32(x) + f32(r),
 // x <- f16(v) (the residual stream is updated in place, ops.ts:41), and the sum of squares takes
 // the unrounded v (ops.ts:42); without: v = f32(x).  normalized = f16(f32(x) * inv * w) with the
-// stored (rounded) x and inv = 1 / sqrt(sum / width + eps) (ops.ts:52-55).
-__global__ __launch_bounds__(256) void rmsnorm_kernel(half_t* x, const half_t* residual, const float* weight,
-                                                      half_t* out, int64_t rows, int width, int64_t x_stride,
-                                                      int64_t r_stride, int64_t out_stride, float eps) {
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const int lane = threadIdx.x & 63;
-  half_t* xr = x + row * x_stride;
-  const half_t* rr = residual ? residual + row * r_stride : nullptr;
+// stored (rounded) x and inv = 1 / sqrt(sum / width + eps) (ops.ts:52-55).  residual_at(c) gives
+// the residual's 8 values at columns c..c+7 (from memory, or from a projection's split-K sums),
+// so both kernels below run the same arithmetic in the same order.
+template <bool RESIDUAL, typename ResidualAt>
+__device__ inline void rmsnorm_row(half_t* xr, ResidualAt residual_at, const float* weight, half_t* out_row,
+                                   int width, float eps, int lane) {
   constexpr int kMaxChunks = kRmsMaxWidth / 512;
   h8 xs[kMaxChunks];
   float ss = 0.f;
@@ -73,8 +70,8 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(half_t* x, const half_t* r
     const int c = 8 * lane + 512 * j;
     if (c < width) {
       h8 a = *reinterpret_cast<const h8*>(xr + c);
-      if (rr) {
-        const h8 b = *reinterpret_cast<const h8*>(rr + c);
+      if (RESIDUAL) {
+        const h8 b = residual_at(c);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const float s = (float)a[e] + (float)b[e];
@@ -102,9 +99,50 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(half_t* x, const half_t* r
       h8 o;
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = (_Float16)((float)xs[j][e] * inv * w[e]);
-      *reinterpret_cast<h8*>(out + row * out_stride + c) = o;
+      *reinterpret_cast<h8*>(out_row + c) = o;
     }
   }
+}
+
+__global__ __launch_bounds__(256) void rmsnorm_kernel(half_t* x, const half_t* residual, const float* weight,
+                                                      half_t* out, int64_t rows, int width, int64_t x_stride,
+                                                      int64_t r_stride, int64_t out_stride, float eps) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  half_t* xr = x + row * x_stride;
+  if (residual) {
+    const half_t* rr = residual + row * r_stride;
+    rmsnorm_row<true>(xr, [&](int c) { return *reinterpret_cast<const h8*>(rr + c); }, weight, out + row * out_stride,
+                      width, eps, lane);
+  } else {
+    rmsnorm_row<false>(xr, [](int) { return h8{}; }, weight, out + row * out_stride, width, eps, lane);
+  }
+}
+
+// A projection's split-K sums as the residual: r = f16(part[0] + part[1] + ...) in chunk order
+// (part: chunks x rows x width fp32, the layout and sums of q4_reduce_kernel), then
+// rmsnorm_row as above: bit for bit the projection's output followed by rmsnorm_kernel.
+__global__ __launch_bounds__(256) void reduce_rmsnorm_kernel(const float* part, int chunks, half_t* x,
+                                                             const float* weight, half_t* out, int64_t rows,
+                                                             int width, int64_t x_stride, int64_t out_stride,
+                                                             float eps) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  const size_t plane = (size_t)rows * (size_t)width;
+  const float* pr = part + (size_t)row * width;
+  auto sums = [&](int c) {
+    f4 s0 = *reinterpret_cast<const f4*>(pr + c), s1 = *reinterpret_cast<const f4*>(pr + c + 4);
+    for (int ch = 1; ch < chunks; ++ch) {
+      s0 = s0 + *reinterpret_cast<const f4*>(pr + (size_t)ch * plane + c);
+      s1 = s1 + *reinterpret_cast<const f4*>(pr + (size_t)ch * plane + c + 4);
+    }
+    return h8{(_Float16)s0[0], (_Float16)s0[1], (_Float16)s0[2], (_Float16)s0[3],
+              (_Float16)s1[0], (_Float16)s1[1], (_Float16)s1[2], (_Float16)s1[3]};
+  };
+  rmsnorm_row<true>(x + row * x_stride, sums, weight, out + row * out_stride, width, eps, lane);
 }
 
 // ---- SwiGLU (SwiGLUKernel, ops.ts:74-102) ------------------------------------------------------
@@ -133,6 +171,14 @@ hipError_t launch_embed_q6k(const int32_t* ids, int64_t tokens, const uint8_t* t
   if (threads <= 0) return hipSuccess;
   hipLaunchKernelGGL(embed_q6k_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, ids, tokens,
                      table, vocab, width, out, out_stride);
+  return hipGetLastError();
+}
+
+hipError_t launch_reduce_rmsnorm(const float* part, int chunks, int rows, int width, const RowNorm& norm,
+                                 hipStream_t stream) {
+  if (rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(reduce_rmsnorm_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream, part, chunks,
+                     norm.x, norm.weight, norm.out, (int64_t)rows, width, norm.x_stride, norm.out_stride, norm.eps);
   return hipGetLastError();
 }
 

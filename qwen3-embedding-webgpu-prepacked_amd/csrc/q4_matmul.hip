@@ -610,7 +610,8 @@ size_t q4_split_bytes(int M, int K, int N) {
 
 template <bool SWIGLU>
 hipError_t launch_q4(const _Float16* x, int64_t ldx, int M, int K, const uint8_t* w, uint32_t w_bytes, int N,
-                     _Float16* y, int64_t ldy, hipStream_t stream, float* ws, size_t ws_bytes) {
+                     _Float16* y, int64_t ldy, hipStream_t stream, float* ws, size_t ws_bytes,
+                     const RowNorm* norm = nullptr, bool* normed = nullptr) {
   const int64_t big_tiles = (int64_t)((M + 127) / 128) * ((N + kQ4TileN - 1) / kQ4TileN);
   const int n_out = SWIGLU ? N / 2 : N;
   const size_t split = SWIGLU ? 0 : q4_split_bytes(M, K, N);
@@ -619,9 +620,16 @@ hipError_t launch_q4(const _Float16* x, int64_t ldx, int M, int K, const uint8_t
     launch_q4_direct<SWIGLU>(x, ldx, M, K, w, w_bytes, N, y, ldy, stream);
   } else if (split && ws && split <= ws_bytes) {
     launch_q4_shape<SWIGLU, 1, 2>(x, ldx, M, K, w, w_bytes, N, y, ldy, stream, ws, chunks);
-    // one row per grid row (M < 64 * kQ4SplitTiles here), 1024 columns per workgroup
-    hipLaunchKernelGGL(q4_reduce_kernel, dim3((unsigned)((N + 1023) / 1024), (unsigned)M), dim3(256), 0, stream, ws,
-                       chunks, M, N, y, ldy);
+    if (norm && N % 8 == 0 && N <= kRmsMaxWidth) {
+      // the sums go straight into the residual add + RMSNorm that follows the projection
+      const hipError_t e = launch_reduce_rmsnorm(ws, chunks, M, N, *norm, stream);
+      if (e != hipSuccess) return e;
+      if (normed) *normed = true;
+    } else {
+      // one row per grid row (M < 64 * kQ4SplitTiles here), 1024 columns per workgroup
+      hipLaunchKernelGGL(q4_reduce_kernel, dim3((unsigned)((N + 1023) / 1024), (unsigned)M), dim3(256), 0, stream,
+                         ws, chunks, M, N, y, ldy);
+    }
   } else if (big_tiles < kQ4SmallLaunch) {
     launch_q4_tiled<SWIGLU, 1>(x, ldx, M, K, w, w_bytes, N, y, ldy, stream);
   } else {
@@ -631,9 +639,10 @@ hipError_t launch_q4(const _Float16* x, int64_t ldx, int M, int K, const uint8_t
 }
 
 hipError_t launch_q4_matmul(const _Float16* x, int64_t ldx, int M, int K, const uint8_t* w, uint32_t w_bytes, int N,
-                            _Float16* y, int64_t ldy, hipStream_t stream, float* ws, size_t ws_bytes) {
+                            _Float16* y, int64_t ldy, hipStream_t stream, float* ws, size_t ws_bytes,
+                            const RowNorm* norm, bool* normed) {
   if (M <= 0 || N <= 0) return hipSuccess;
-  return launch_q4<false>(x, ldx, M, K, w, w_bytes, N, y, ldy, stream, ws, ws_bytes);
+  return launch_q4<false>(x, ldx, M, K, w, w_bytes, N, y, ldy, stream, ws, ws_bytes, norm, normed);
 }
 
 // y [M, n_inter] = swiglu of the [gate | up] projection; the weight has 2 n_inter rows and
