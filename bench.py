@@ -344,17 +344,19 @@ def rope_timing(reps):
     ctx.close()
 
 
-def q4_timing(reps):
+Q4_SHAPES = (("qkv", 1024, 4096), ("attn_out", 2048, 1024), ("gate_up", 1024, 6144), ("down", 3072, 1024))
+
+
+def q4_timing(reps, ms=(8000,)):
     """The projection kernel alone (not the headline metric): qattn_q4_matmul at the shapes one
-    layer of the 16 x 500 packing multiplies (M = 8000 tokens): the fused QKV projection
+    layer multiplies for M tokens (8000 = one 16 x 500 packing): the fused QKV projection
     (K 1024 -> N 4096), the attention output projection (2048 -> 1024), the gate/up projection
     (1024 -> 6144) and the down projection (3072 -> 1024).  Random Q4_0 records, `reps` launches
     per shape between HIP events; algorithmic FLOP = 2 M N K.  One JSON line per shape."""
     q = load_binding()
     ctx = q.Context(0)
     rng = np.random.default_rng(0)
-    M = 8000
-    for name, K, N in (("qkv", 1024, 4096), ("attn_out", 2048, 1024), ("gate_up", 1024, 6144), ("down", 3072, 1024)):
+    for M, (name, K, N) in ((M, s) for M in ms for s in Q4_SHAPES):
         nbytes = q.lib().qattn_q4_compact_bytes(K, N)
         wts = rng.integers(0, 256, size=nbytes, dtype=np.uint8)
         rec = wts.reshape(-1, 20)
@@ -381,6 +383,33 @@ def q4_timing(reps):
         e0.destroy()
         e1.destroy()
     ctx.close()
+
+
+def dense_gemm_timing(reps, ms=(8000,)):
+    """A reference ceiling for the projection shapes, not part of the path: torch.matmul on dense
+    fp16 operands (hipBLASLt's GEMM, no dequantisation) at the shapes q4_timing runs, `reps`
+    launches between events after 3 warm-ups.  Runs without libqattn.so in the process: torch
+    brings its own HIP runtime, which finds no device once the library's runtime holds it."""
+    import torch
+    torch.manual_seed(0)
+    for M, (name, K, N) in ((M, s) for M in ms for s in Q4_SHAPES):
+        x = torch.randn(M, K, device="cuda", dtype=torch.float16)
+        wt = (torch.randn(N, K, device="cuda", dtype=torch.float16) * 0.02).t()
+        for _ in range(3):
+            torch.matmul(x, wt)
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0.record()
+        for _ in range(reps):
+            torch.matmul(x, wt)
+        t1.record()
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) * 1000.0 / reps
+        flop = 2.0 * M * N * K
+        print(json.dumps({"kernel": "torch.matmul fp16 (hipBLASLt)", "shape": name, "M": M, "K": K, "N": N,
+                          "launches": reps, "us_per_launch": round(us, 2), "TFLOP/s": round(flop / us / 1e6, 1),
+                          "frac_of_fp16_peak": round(flop / us / 1e6 / PEAK_FP16_TFLOPS, 3)}), flush=True)
+        del x, wt
 
 
 def synthetic_model(ctx, q, n_layers, vocab, seed=0, scale=0.005, flags=0):
@@ -619,6 +648,11 @@ def main():
                     help="only time N launches of the last-token pool kernel per width and exit")
     ap.add_argument("--q4", type=int, default=0, metavar="N",
                     help="only time N launches of the Q4_0 dequant-GEMM per projection shape and exit")
+    ap.add_argument("--q4-m", default="8000", metavar="M[,M...]",
+                    help="token counts for --q4 (default 8000, one 16 x 500 packing)")
+    ap.add_argument("--dense-gemm", type=int, default=0, metavar="N",
+                    help="only time N launches of torch.matmul (hipBLASLt) on dense fp16 operands of each "
+                         "--q4-m projection shape (a reference ceiling, without libqattn.so) and exit")
     ap.add_argument("--rope", type=int, default=0, metavar="N",
                     help="only time N launches of the fused QK-norm + RoPE producer and exit")
     ap.add_argument("--model", type=int, default=0, metavar="N",
@@ -646,7 +680,10 @@ def main():
         rope_timing(args.rope)
         return
     if args.q4:
-        q4_timing(args.q4)
+        q4_timing(args.q4, tuple(int(m) for m in args.q4_m.split(",")))
+        return
+    if args.dense_gemm:
+        dense_gemm_timing(args.dense_gemm, tuple(int(m) for m in args.q4_m.split(",")))
         return
     if args.pool:
         pool_timing(args.pool)
