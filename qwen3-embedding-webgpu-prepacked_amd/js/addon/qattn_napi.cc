@@ -66,6 +66,7 @@ struct Buf {
   Ctx* owner = nullptr;
   void* ptr = nullptr;
   size_t bytes = 0;
+  int reads_in_flight = 0;  // readAfterAsync copies from this buffer not yet settled
 };
 // A run holds a reference on each buffer bound to it (so none is collected before the run), and
 // the largest token / sequence counts those buffers can take (updateRun checks new batches
@@ -320,6 +321,11 @@ napi_value Free(napi_env env, napi_callback_info info) {
   if (!args_of(env, info, 1, argv)) return nullptr;
   Buf* b = get_external<Buf>(env, argv[0], "device buffer");
   if (!b) return nullptr;
+  if (b->reads_in_flight > 0) {
+    // a worker thread would copy from freed (or reallocated) device memory
+    napi_throw_error(env, nullptr, "device buffer has asynchronous reads in flight; await them first");
+    return nullptr;
+  }
   if (b->ptr && b->owner->ctx) {
     int rc = qattn_buffer_free(b->owner->ctx, b->ptr);
     if (rc) return throw_qattn(env, rc, b->owner->ctx);
@@ -1231,6 +1237,7 @@ struct ReadWork {
   napi_async_work work = nullptr;
   napi_deferred deferred = nullptr;
   napi_ref buf_ref = nullptr, evt_ref = nullptr, dst_ref = nullptr;
+  Buf* buf = nullptr;  // kept alive by buf_ref
   Evt* evt = nullptr;
   qattn_ctx* ctx = nullptr;
   const void* src = nullptr;
@@ -1262,6 +1269,7 @@ void read_complete(napi_env env, napi_status, void* data) {
     napi_create_error(env, nullptr, m, &err);
     napi_reject_deferred(env, w->deferred, err);
   }
+  --w->buf->reads_in_flight;
   napi_delete_reference(env, w->buf_ref);
   napi_delete_reference(env, w->evt_ref);
   napi_delete_reference(env, w->dst_ref);
@@ -1305,6 +1313,7 @@ napi_value ReadAfterAsync(napi_env env, napi_callback_info info) {
     return nullptr;
   }
   auto* w = new ReadWork();
+  w->buf = b;
   w->evt = e;
   w->ctx = b->owner->ctx;
   w->src = b->ptr;
@@ -1314,6 +1323,7 @@ napi_value ReadAfterAsync(napi_env env, napi_callback_info info) {
   NAPI_OK(env, napi_create_reference(env, argv[1], 1, &w->evt_ref));
   NAPI_OK(env, napi_create_reference(env, argv[2], 1, &w->dst_ref));
   ++e->waiters;
+  ++b->reads_in_flight;
   ++b->owner->refs;  // the context outlives the wait
   ++b->owner->async_busy;
   napi_value promise, name;

@@ -56,6 +56,8 @@ async function main() {
   const pending = small.complete(ticket);
   assert.throws(() => small.destroy(), /in flight/);
   assert.throws(() => runtime.context.addon.destroyContext(runtime.context.handle), /in flight/);
+  // nor does the buffer being read back, freed directly through the addon
+  assert.throws(() => runtime.context.addon.free(small.slots[0].out.handle), /in flight/);
   const [tiny] = await pending;
   assert.ok(Math.abs(Math.hypot(...tiny) - 1) < 1e-3);
   small.destroy();
