@@ -102,7 +102,8 @@ int qattn_buffer_fill_u16(qattn_ctx* ctx, void* dst, uint16_t value, size_t coun
  * once the work recorded before event `after` (qattn_event_record on the context stream) has
  * finished, on a stream of the context's own for readbacks, so work enqueued on the context stream
  * after that event (the next batch) is not waited for.  Blocks until the copy is done; safe to call
- * from another host thread while this one enqueues. */
+ * from another host thread while this one enqueues, as long as src stays allocated and ctx alive
+ * until it returns. */
 int qattn_buffer_read_after(qattn_ctx* ctx, qattn_event_t after, const void* src, size_t offset,
                             void* dst, size_t bytes);
 
