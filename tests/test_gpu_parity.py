@@ -359,6 +359,24 @@ def test_causal_mask_kind_long(ctx, qattn, oracle):
     case.free()
 
 
+@pytest.mark.timeout(300)
+@pytest.mark.parametrize("mask", [0, 1])
+def test_one_sequence_past_8192_tokens(ctx, qattn, oracle, mask):
+    """One 12,000-token sequence.  Above 8192 tokens the reference switches to a chunked two-pass
+    path (ops.ts:328-342); this kernel plans it like any other length, with its longest items split
+    over several workgroups.  Sampled rows, the rows around the 8192 boundary and the last row
+    against the f64 oracle, under the causal and the prefix + window masks."""
+    L = 12000
+    rows = np.unique(np.concatenate([np.arange(0, L, 97), [63, 64, 8191, 8192, 8193, L - 1]]))
+    print(f"1x{L} mask {mask}", flush=True)
+    case, (q, k, v, cu), got, exact = _exact_and_gpu(ctx, qattn, oracle, [L], config=3, mask=mask, rows=rows)
+    compare(got[rows], exact, f"1x{L} mask {mask}")
+    if mask == 1:  # the rows past prefix + window really drop keys: far from the causal answer
+        causal = oracle.attention_exact(q, k, v, cu, 0, 176, 432, rows=np.array([8192]))
+        assert np.abs(f16(got[8192]).reshape(causal.shape) - causal).max() > 1e-2
+    case.free()
+
+
 @pytest.mark.parametrize("P,W", [(7, 50), (0, 33), (64, 1), (200, 64), (1, 1)])
 def test_other_prefix_window(ctx, qattn, oracle, P, W):
     case, _, got, exact = _exact_and_gpu(ctx, qattn, oracle, [333, 80], P=P, W=W)
